@@ -1,0 +1,193 @@
+// Producers of the int8 GEMM inputs: per-row activation quantization (reference kernels/csrc/encoder_ops.cu:18-54
+// store_q8 / quantize_rows) and LayerNorm(s) with int8 output (encoder_ops.cu:57-79, layernorm.cuh:6-43).
+//
+// One wave per row; each lane holds up to VEC 8-element chunks of the row in registers (16-byte loads), so a row is
+// read once and written once. The quantization arithmetic is the reference's: mx = max|bf16 x|, s = mx > 0 ?
+// mx / 127 : 1, inv = 1 / s (both correctly rounded fp32 divisions), q = rint_half_even(clamp(x * inv, +-127)).
+#include "common.h"
+#include "cohere_hip.h"
+
+#include <string>
+
+namespace {
+
+template <int VEC>
+struct Row {
+  float v[VEC][8];
+};
+
+template <int VEC>
+DEVI void load_row(const uint16_t* x, int cols, int lane, Row<VEC>& r) {
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    uint4 u = make_uint4(0, 0, 0, 0);
+    if (c < cols) u = *reinterpret_cast<const uint4*>(x + c);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r.v[i][2 * k] = __uint_as_float(w[k] << 16);
+      r.v[i][2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+    }
+  }
+}
+
+// the row (already bf16 values) as int8 with one scale per row
+template <int VEC>
+DEVI void store_q8(const Row<VEC>& r, int cols, int lane, int8_t* q, float* scale) {
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(r.v[i][k]));
+  mx = wave_max_xor(mx, 64);
+  const float s = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / s;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c >= cols) continue;
+    uint32_t w[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int v = (int)rintf(fminf(fmaxf(r.v[i][k] * inv, -127.f), 127.f));
+      w[k >> 2] |= (uint32_t)(v & 0xff) << ((k & 3) * 8);
+    }
+    *reinterpret_cast<uint2*>(q + c) = make_uint2(w[0], w[1]);
+  }
+  if (lane == 0) *scale = s;
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                            int8_t* __restrict__ q, int64_t ldq, float* __restrict__ s,
+                                                            int rows, int cols) {
+  const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
+  if (row >= rows) return;
+  Row<VEC> r;
+  load_row<VEC>(x + (int64_t)row * ldx, cols, lane, r);
+  store_q8<VEC>(r, cols, lane, q + (int64_t)row * ldq, s + row);
+}
+
+DEVI float wave_sum(float v) {
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// LayerNorm of the row in place (fp32 statistics over the bf16 inputs), the result rounded to bf16
+template <int VEC>
+DEVI void ln_row(Row<VEC>& r, int cols, int lane, const uint16_t* w, const uint16_t* b, float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += r.v[i][k];
+  const float mean = wave_sum(s) / (float)cols;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    if ((i * 64 + lane) * 8 >= cols) continue;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float d = r.v[i][k] - mean;
+      q += d * d;
+    }
+  }
+  const float rstd = 1.f / sqrtf(wave_sum(q) / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c >= cols) continue;
+    const uint4 wv = *reinterpret_cast<const uint4*>(w + c), bv = *reinterpret_cast<const uint4*>(b + c);
+    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float wk = __uint_as_float(k & 1 ? ww[k >> 1] & 0xffff0000u : ww[k >> 1] << 16);
+      const float bk = __uint_as_float(k & 1 ? bb[k >> 1] & 0xffff0000u : bb[k >> 1] << 16);
+      r.v[i][k] = round_bf(__builtin_fmaf((r.v[i][k] - mean) * rstd, wk, bk));
+    }
+  }
+}
+
+template <int VEC>
+DEVI void store_row(const Row<VEC>& r, int cols, int lane, uint16_t* x) {
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c >= cols) continue;
+    uint4 u;
+    u.x = pack_bf2(r.v[i][0], r.v[i][1]);
+    u.y = pack_bf2(r.v[i][2], r.v[i][3]);
+    u.z = pack_bf2(r.v[i][4], r.v[i][5]);
+    u.w = pack_bf2(r.v[i][6], r.v[i][7]);
+    *reinterpret_cast<uint4*>(x + c) = u;
+  }
+}
+
+template <int VEC, bool TWO>
+__global__ void __launch_bounds__(256) layernorm_q8_kernel(uint16_t* x, int64_t ldx, const uint16_t* w1,
+                                                           const uint16_t* b1, float eps1, const uint16_t* w2,
+                                                           const uint16_t* b2, float eps2, int8_t* hq, int64_t ldq,
+                                                           float* hs, int rows, int cols) {
+  const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
+  if (row >= rows) return;
+  Row<VEC> r;
+  uint16_t* xr = x + (int64_t)row * ldx;
+  load_row<VEC>(xr, cols, lane, r);
+  ln_row<VEC>(r, cols, lane, w1, b1, eps1);
+  if constexpr (TWO) {
+    store_row<VEC>(r, cols, lane, xr);
+    ln_row<VEC>(r, cols, lane, w2, b2, eps2);
+  }
+  store_q8<VEC>(r, cols, lane, hq + (int64_t)row * ldq, hs + row);
+}
+
+bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+}  // namespace
+
+extern "C" int cohere_quantize_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int64_t rows,
+                                    int64_t cols, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 2048,
+                 "quantize_rows: cols must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(x && q && s && al16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7) == 0 && ldq % 8 == 0,
+                 "quantize_rows: rows must be aligned");
+  if (rows == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int grid = (int)((rows + 3) / 4), vec = (int)((cols + 511) / 512);
+  switch (vec) {
+    case 1: quantize_rows_kernel<1><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
+    case 2: quantize_rows_kernel<2><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
+    case 3: quantize_rows_kernel<3><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
+    default: quantize_rows_kernel<4><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
+  }
+  return cohere::check_launch("quantize_rows");
+}
+
+extern "C" int cohere_layernorm_q8(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1,
+                                   const uint16_t* w2, const uint16_t* b2, float eps2, int8_t* hq, int64_t ldq,
+                                   float* hs, int64_t rows, int64_t cols, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 2048,
+                 "layernorm_q8: cols must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(x && w1 && b1 && hq && hs && al16(x) && ldx % 8 == 0 && al16(w1) && al16(b1) &&
+                     (reinterpret_cast<uintptr_t>(hq) & 7) == 0 && ldq % 8 == 0,
+                 "layernorm_q8: rows must be aligned");
+  COHERE_REQUIRE(!w2 || (b2 && al16(w2) && al16(b2)), "layernorm_q8: second LayerNorm needs aligned w2 and b2");
+  if (rows == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int grid = (int)((rows + 3) / 4), vec = (int)((cols + 511) / 512);
+#define LNQ(V)                                                                                                    \
+  (w2 ? layernorm_q8_kernel<V, true><<<grid, 256, 0, st>>>(x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs,     \
+                                                            (int)rows, (int)cols)                                 \
+      : layernorm_q8_kernel<V, false><<<grid, 256, 0, st>>>(x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs,    \
+                                                             (int)rows, (int)cols))
+  switch (vec) {
+    case 1: LNQ(1); break;
+    case 2: LNQ(2); break;
+    case 3: LNQ(3); break;
+    default: LNQ(4); break;
+  }
+#undef LNQ
+  return cohere::check_launch("layernorm_q8");
+}

@@ -1,0 +1,193 @@
+"""The gfx950 kernels of the quantized-GEMM path behind the reference's `ext` call surface.
+
+Drop-in for the reference's kernels/cuda_ext.py (`ext` object and `EPI_*` constants, cuda_ext.py:26-28) for the
+functions of this path: the methods keep the names, argument order and meaning of the pybind11 module
+(kernels/csrc/bindings.cpp:26-62), validate dtypes and strides as its TORCH_CHECKs do, launch on the current stream,
+and raise RuntimeError on a rejected call. Underneath is libcohere_hip.so, the C ABI of include/cohere_hip.h, loaded
+with ctypes; nothing here computes on the host.
+
+    from kernels.cuda_ext import EPI_BIAS, EPI_RESID, ext
+    ext.gemm_i8(a, sa, 1280, w, sw, bias, out, EPI_BIAS, None, 1.0, None, 0)
+
+The library is built in-tree (cohere-inference_amd/csrc/build.py, run by __graft_entry__.build()); importing this
+module without it raises ImportError -- there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG, "lib", "libcohere_hip.so")
+
+EPI_BIAS, EPI_SILU, EPI_RELU, EPI_RESID, EPI_GLU, EPI_SILU_Q8, EPI_CONV_RELU = range(7)
+EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the reference
+
+# every symbol include/cohere_hip.h declares
+EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_layernorm_q8", "cohere_dec_w8_linear",
+           "cohere_linear_bf16", "cohere_last_error", "cohere_version", "cohere_set_gemm_tile")
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(f"libcohere_hip.so not built ({path}); run __graft_entry__.build() or "
+                          "python cohere-inference_amd/csrc/build.py")
+    lib = ctypes.CDLL(path)
+    P, I64, I32, F = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_float
+    sig = {
+        "cohere_gemm_i8": [P, I64, P, I64, I64, P, P, P, P, I64, I32, P, I64, F, P, I64, I64, I64, I64, I32, P],
+        "cohere_gemm_sp": [P, I64, P, I64, I64, P, P, P, P, P, I64, I32, P, I64, F, P, I64, I64, I64, I64, I32, P],
+        "cohere_quantize_rows": [P, I64, P, I64, P, I64, I64, P],
+        "cohere_layernorm_q8": [P, I64, P, P, F, P, P, F, P, I64, P, I64, I64, P],
+        "cohere_dec_w8_linear": [P, I64, P, P, P, P, I64, I32, I64, I64, P, I64, P, I64, I64, I64, I64, P],
+        "cohere_linear_bf16": [P, I64, P, P, P, I64, I32, I64, I64, I64, P],
+        "cohere_set_gemm_tile": [I32],
+    }
+    for name, args in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    lib.cohere_last_error.restype = ctypes.c_char_p
+    lib.cohere_last_error.argtypes = []
+    lib.cohere_version.restype = ctypes.c_char_p
+    lib.cohere_version.argtypes = []
+    return lib
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class _Ext:
+    """The methods of the reference's `ext` on this path, on gfx950."""
+
+    def __init__(self, lib: ctypes.CDLL):
+        self._lib = lib
+
+    def _call(self, name: str, *args) -> None:
+        rc = getattr(self._lib, name)(*args)
+        if rc != 0:
+            raise RuntimeError(self._lib.cohere_last_error().decode())
+
+    @property
+    def version(self) -> str:
+        return self._lib.cohere_version().decode()
+
+    def set_gemm_tile(self, tile: int) -> int:
+        """Tuning hook: force a gfx950 GEMM tile (-1 = automatic). Results never depend on it."""
+        return self._lib.cohere_set_gemm_tile(int(tile))
+
+    # ---- int8 GEMMs (bindings.cpp:41-43, 59-61) ----------------------------------------------------------------------
+
+    def gemm_i8(self, a, sa, group, w, sw, bias, out, epi, resid, alpha, qs, cfg):
+        """out = epilogue(dequant(a @ w^T) + bias); a int8 (M, K) with sa (M, K / group) fp32, w int8 (N, K) with sw
+        (N) fp32 (reference kernels/csrc/gemm_int8.cu:349-391). EPI_SILU_Q8 writes int8 out and qs."""
+        _check(a.dtype == torch.int8 and w.dtype == torch.int8 and sa.dtype == torch.float32 and
+               sw.dtype == torch.float32, "gemm_i8: a, w int8 and sa, sw fp32 expected")
+        _check(a.dim() == 2 and a.stride(1) == 1 and w.is_contiguous() and out.stride(1) == 1 and sa.stride(1) == 1,
+               "gemm_i8: a, out, sa need unit column stride and w must be contiguous")
+        M, K = a.shape
+        _check(w.shape[1] == K and K % 64 == 0 and group % 64 == 0 and K % group == 0,
+               "gemm_i8: K must match, be a multiple of 64 and of group")
+        _check(bias is None or bias.dtype == torch.bfloat16, "gemm_i8: bias must be bf16")
+        if epi == EPI_SILU_Q8:
+            _check(qs is not None and out.dtype == torch.int8, "gemm_i8: SILU_Q8 needs int8 out and qs")
+        elif epi == EPI_I32:
+            _check(out.dtype == torch.int32, "gemm_i8: EPI_I32 needs int32 out")
+        else:
+            _check(out.dtype == torch.bfloat16, "gemm_i8: out must be bf16")
+        _check(epi != EPI_RESID or resid is not None, "gemm_i8: residual epilogue needs resid")
+        if M == 0:
+            return
+        self._call("cohere_gemm_i8", _ptr(a), a.stride(0), _ptr(sa), sa.stride(0), int(group), _ptr(w), _ptr(sw),
+                   _ptr(bias), _ptr(out), out.stride(0), int(epi), _ptr(resid),
+                   resid.stride(0) if resid is not None else 0, float(alpha), _ptr(qs),
+                   qs.stride(0) if qs is not None else 0, M, w.shape[0], K, int(cfg), _stream())
+
+    def gemm_sp(self, x, sx, group, wc, e, sw, bias, r, out, alpha, cfg):
+        """out = r + alpha * bf16(dequant(x @ w^T) + bias) with w 2:4 sparse as compress_24 stores it (wc (N, K/2)
+        int8, e (N, K/32) int32); reference kernels/csrc/gemm_sparse.cu:211-253."""
+        self.gemm_sp_epi(x, sx, group, wc, e, sw, bias, out, EPI_RESID, r, alpha, None, cfg)
+
+    def gemm_sp_epi(self, x, sx, group, wc, e, sw, bias, out, epi, resid, alpha, qs, cfg):
+        """The sparse GEMM with gemm_i8's epilogues (BIAS, RESID, GLU, SILU_Q8, I32): the reference's gemm_sp widened
+        (its kernel has the residual epilogue only). Same results as gemm_i8 on the decompressed weights."""
+        _check(x.dtype == torch.int8 and wc.dtype == torch.int8 and e.dtype == torch.int32 and
+               sx.dtype == torch.float32 and sw.dtype == torch.float32, "gemm_sp: dtypes")
+        _check(x.stride(1) == 1 and wc.is_contiguous() and e.is_contiguous() and sx.stride(1) == 1 and
+               out.stride(1) == 1 and (resid is None or resid.stride(1) == 1), "gemm_sp: strides")
+        M, K = x.shape
+        _check(wc.shape[1] * 2 == K and e.shape[1] * 32 == K and K % 128 == 0 and group % 128 == 0 and
+               K % group == 0, "gemm_sp: K must be a multiple of 128 and of group, wc (N, K/2), e (N, K/32)")
+        _check(epi != EPI_RESID or resid is not None, "gemm_sp: residual epilogue needs r")
+        _check(epi != EPI_SILU_Q8 or (qs is not None and out.dtype == torch.int8), "gemm_sp: SILU_Q8 needs qs")
+        if M == 0:
+            return
+        self._call("cohere_gemm_sp", _ptr(x), x.stride(0), _ptr(sx), sx.stride(0), int(group), _ptr(wc), _ptr(e),
+                   _ptr(sw), _ptr(bias), _ptr(out), out.stride(0), int(epi), _ptr(resid),
+                   resid.stride(0) if resid is not None else 0, float(alpha), _ptr(qs),
+                   qs.stride(0) if qs is not None else 0, M, wc.shape[0], K, int(cfg), _stream())
+
+    # ---- int8 activation producers (bindings.cpp:44-46, 73-75) --------------------------------------------------
+
+    def quantize_rows(self, x, q, s):
+        """bf16 rows -> int8 with one fp32 scale per row (reference encoder_ops.cu:545-553)."""
+        _check(x.dtype == torch.bfloat16 and x.stride(1) == 1 and q.is_contiguous() and q.dtype == torch.int8 and
+               s.dtype == torch.float32, "quantize_rows: bf16 x, int8 contiguous q, fp32 s")
+        rows, cols = x.shape
+        _check(tuple(q.shape) == (rows, cols) and s.numel() >= rows, "quantize_rows: shapes")
+        self._call("cohere_quantize_rows", _ptr(x), x.stride(0), _ptr(q), cols, _ptr(s), rows, cols, _stream())
+
+    def layernorm_q8(self, x, w1, b1, eps1, w2, b2, eps2, hq, hs):
+        """h = LN(x) as int8 hq + per-row scale hs; with w2: x = LN1(x) in place, h = LN2(x) (encoder_ops.cu:522)."""
+        _check(x.dtype == torch.bfloat16 and x.stride(1) == 1 and hq.is_contiguous() and hq.dtype == torch.int8 and
+               hs.dtype == torch.float32, "layernorm_q8: dtypes/strides")
+        rows, cols = x.shape
+        _check(hq.shape[1] == cols and hs.numel() >= rows, "layernorm_q8: shapes")
+        self._call("cohere_layernorm_q8", _ptr(x), x.stride(0), _ptr(w1), _ptr(b1), float(eps1), _ptr(w2), _ptr(b2),
+                   float(eps2), _ptr(hq), cols, _ptr(hs), rows, cols, _stream())
+
+    # ---- decoder projections (bindings.cpp:55-56) -----------------------------------------------------------
+
+    def dec_w8_linear(self, x, w, sw, bias, y, relu, bn, splits, ws, counters):
+        """y = x @ dequant(w)^T + bias (relu), M <= 64, w in prepare_w8's layout (reference dec_w8.cu:205-234)."""
+        _check(x.dtype == torch.bfloat16 and w.dtype == torch.uint8 and sw.dtype == torch.float32 and
+               y.dtype == torch.bfloat16, "dec_w8_linear: dtypes")
+        M, K = x.shape
+        N = w.shape[0]
+        _check(M <= 64 and x.stride(1) == 1 and w.is_contiguous() and w.shape[1] == K and y.stride(1) == 1,
+               "dec_w8_linear: M <= 64, unit column strides, contiguous w")
+        if M == 0:
+            return
+        self._call("cohere_dec_w8_linear", _ptr(x), x.stride(0), _ptr(w), _ptr(sw), _ptr(bias), _ptr(y), y.stride(0),
+                   int(bool(relu)), int(bn), int(splits), _ptr(ws), ws.numel() if ws is not None else 0,
+                   _ptr(counters), counters.numel() if counters is not None else 0, M, N, K, _stream())
+
+    def linear_bf16(self, x, w, bias, y, relu=False):
+        """y = x @ w^T + bias (relu) for bf16 weights, M <= 64: the decoder's o / cross-q / cross-o projections
+        (the reference runs them in Triton, kernels/decoder_kernels.py:55-66)."""
+        _check(x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and y.dtype == torch.bfloat16,
+               "linear_bf16: bf16 expected")
+        M, K = x.shape
+        _check(M <= 64 and x.stride(1) == 1 and w.is_contiguous() and w.shape[1] == K and y.stride(1) == 1,
+               "linear_bf16: M <= 64, unit column strides, contiguous w")
+        if M == 0:
+            return
+        self._call("cohere_linear_bf16", _ptr(x), x.stride(0), _ptr(w), _ptr(bias), _ptr(y), y.stride(0),
+                   int(bool(relu)), M, w.shape[0], K, _stream())
+
+
+_lib = load_library()
+ext = _Ext(_lib)

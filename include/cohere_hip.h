@@ -1,0 +1,105 @@
+/* C ABI of the MI355X (gfx950) quantized-GEMM path of cohere-inference.
+ *
+ * Every entry point takes raw device pointers, element strides and sizes, and a HIP stream (hipStream_t passed as
+ * void*; NULL is the default stream). Every call only enqueues work on that stream: no host synchronisation, no
+ * device allocation, so each is safe inside HIP graph capture. Return value: 0 on success, nonzero on a rejected
+ * argument or a failed launch; cohere_last_error() then describes it (thread-local, valid until the next call on the
+ * same thread).
+ *
+ * bf16 tensors are passed as uint16_t bit patterns. All matrices are row-major with the given row strides (in
+ * elements); the innermost stride is 1.
+ *
+ * Epilogue codes (kernels/cuda_ext.py:28 of the reference: EPI_BIAS, EPI_SILU, EPI_RELU, EPI_RESID, EPI_GLU,
+ * EPI_SILU_Q8, EPI_CONV_RELU = range(7)); the int8 GEMMs accept BIAS, RESID, GLU, SILU_Q8, and COHERE_EPI_I32 (7),
+ * which writes the raw int32 accumulators: a parity hook with no counterpart in the reference.
+ */
+#ifndef COHERE_HIP_H
+#define COHERE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  COHERE_EPI_BIAS = 0,
+  COHERE_EPI_SILU = 1,
+  COHERE_EPI_RELU = 2,
+  COHERE_EPI_RESID = 3,
+  COHERE_EPI_GLU = 4,
+  COHERE_EPI_SILU_Q8 = 5,
+  COHERE_EPI_CONV_RELU = 6,
+  COHERE_EPI_I32 = 7
+};
+
+/* Replaces gemm_i8 (reference kernels/csrc/gemm_int8.cu:351-391, bound at kernels/csrc/bindings.cpp:66).
+ * out = epilogue(dequant(a @ w^T) + bias): a int8 [M, K] (lda), sa fp32 [M, K / group] (ldsa), w int8 [N, K]
+ * contiguous, sw fp32 [N], bias bf16 [N] or NULL.
+ *   BIAS     out bf16 [M, N]
+ *   RESID    out = resid + alpha * bf16(v), bf16 [M, N]; out may alias resid
+ *   GLU      out bf16 [M, N / 2] from interleaved (a, gate) rows of w
+ *   SILU_Q8  out int8 [M, N] and qs fp32 [M, N / G] (ldqs), G = the column tile of the reference config cfg
+ *            (64 for cfg 5 and 9, 256 for 4, 6 and 8, else 128; 256 when cfg < 0)
+ *   I32      out int32 [M, N] raw accumulators (group == K only)
+ * Requirements: K % 64 == 0, group % 64 == 0, K % group == 0, N % 64 == 0. cfg is the reference's tile-config id
+ * (0, 1, 3-10; unknown ids are rejected) or -1; it never changes the result (tiles are chosen for gfx950 here). */
+int cohere_gemm_i8(const int8_t* a, int64_t lda, const float* sa, int64_t ldsa, int64_t group, const int8_t* w,
+                   const float* sw, const uint16_t* bias, void* out, int64_t ldc, int32_t epi, const uint16_t* resid,
+                   int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N, int64_t K, int32_t cfg,
+                   void* stream);
+
+/* Replaces gemm_sp (reference kernels/csrc/gemm_sparse.cu:214-253, bound at kernels/csrc/bindings.cpp:84) and
+ * widens it to gemm_i8's epilogues. x int8 [M, K] (ldx) with sx fp32 [M, K / group] (ldsx); the 2:4 weights as
+ * kernels/sparse.py compress_24 stores them: wc int8 [N, K / 2] kept values, e int32 [N, K / 32] selectors (a nibble
+ * i0 | i1 << 2 per group of four, lowest K in the lowest nibble) -- exactly the CDNA4 SMFMAC A operand and index
+ * format, used as is. Epilogues and outputs as cohere_gemm_i8. Requirements: K % 128 == 0, group % 128 == 0,
+ * K % group == 0, N % 64 == 0. The result equals cohere_gemm_i8 on the decompressed weights, bit for bit.
+ * cfg: the reference's sparse config id (0-4) or -1. */
+int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, int64_t group, const int8_t* wc,
+                   const int32_t* e, const float* sw, const uint16_t* bias, void* out, int64_t ldc, int32_t epi,
+                   const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N,
+                   int64_t K, int32_t cfg, void* stream);
+
+/* Replaces quantize_rows (reference kernels/csrc/encoder_ops.cu:545-553, bound at bindings.cpp:70): bf16 rows x
+ * [rows, cols] (ldx) -> int8 q [rows, cols] (ldq) and fp32 s [rows]; one scale per row, absmax / 127. */
+int cohere_quantize_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int64_t rows, int64_t cols,
+                         void* stream);
+
+/* Replaces layernorm_q8 (reference kernels/csrc/encoder_ops.cu:522-543, bound at bindings.cpp:71): h = LN(x) as int8
+ * hq with per-row scale hs; with w2 != NULL, x = LN1(x) in place and h = LN2(x). bf16 x [rows, cols] (ldx),
+ * weights/biases bf16 [cols]. */
+int cohere_layernorm_q8(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1,
+                        const uint16_t* w2, const uint16_t* b2, float eps2, int8_t* hq, int64_t ldq, float* hs,
+                        int64_t rows, int64_t cols, void* stream);
+
+/* Replaces dec_w8_linear (reference kernels/csrc/dec_w8.cu:207-234, bound at bindings.cpp:76). y bf16 [M, N] (ldy) =
+ * x bf16 [M, K] (ldx) @ dequant(w)^T + bias (ReLU), M <= 64; w uint8 [N, K] in prepare_w8's layout (int8 + 128,
+ * bytes permuted within every 16 of K, reference kernels/stream_decoder.py:38-48), sw fp32 [N]. bn (16, 32, 64) and
+ * splits (1..16, K % (128 * splits) == 0) are the reference's tuning knobs; splits > 1 needs ws (fp32, >= N/bn *
+ * splits * 64 * bn elements) and counters (int32, >= N/bn, zero on the first call; the kernel leaves them zero). */
+int cohere_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* sw, const uint16_t* bias,
+                         uint16_t* y, int64_t ldy, int32_t relu, int64_t bn, int64_t splits, float* ws, int64_t ws_len,
+                         int32_t* counters, int64_t counters_len, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Replaces the bf16 decoder projections (reference kernels/decoder_kernels.py:55-66 `linear`, Triton for <= 32 rows;
+ * kernels/stream_decoder.py:23-27 F.linear above): y bf16 [M, N] = x bf16 [M, K] @ w bf16 [N, K]^T + bias (ReLU),
+ * M <= 64, fp32 accumulation. */
+int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
+                       int64_t ldy, int32_t relu, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* The last error on this thread ("" when none). */
+const char* cohere_last_error(void);
+
+/* Library version string. */
+const char* cohere_version(void);
+
+/* Tuning hook (no counterpart in the reference): force the gfx950 tile of the int8 GEMMs (-1 = automatic choice by
+ * shape). Used by bench.py's sweeps; results never depend on it. Returns the number of tiles available. */
+int cohere_set_gemm_tile(int32_t tile);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COHERE_HIP_H */

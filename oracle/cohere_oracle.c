@@ -1,0 +1,298 @@
+/* CPU restatement of cohere-inference's quantized-GEMM arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY. This file is the checker the parity tests, smoke() and bench.py's cpu_baseline leg
+ * compare the HIP kernels against; the product path never calls it.
+ *
+ * Every function follows a cited reference location (paths relative to the reference repository root) and keeps its
+ * roundings: fp32 divides and multiplies are single IEEE operations, fmaf() is the correctly rounded fused multiply-add
+ * (built with -ffp-contract=off so the compiler adds no others), bf16 conversions round to nearest even, and
+ * rintf() rounds half to even under the default rounding mode.
+ *
+ * Pinning (what checks each function against something other than itself) is listed in oracle/__init__.py.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+enum { EPI_BIAS = 0, EPI_SILU = 1, EPI_RELU = 2, EPI_RESID = 3, EPI_GLU = 4, EPI_SILU_Q8 = 5, EPI_I32 = 7 };
+
+static inline float bf2f(uint16_t h) {
+  uint32_t u = (uint32_t)h << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static inline uint16_t f2bf(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40); /* quiet NaN */
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static inline float round_bf(float f) { return bf2f(f2bf(f)); }
+
+/* the textbook logistic in fp32 (the reference's kernels use a fast exp; the tests allow for the difference) */
+static inline float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+static void set_threads(int nthreads) {
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+}
+
+/* a1: kernels/fast_encoder.py:60-63 quantize_rows (weights, per output channel):
+ * s = max(amax|w|, 1e-12) / 127; q = clamp(round_half_even(w / s), -127, 127). w holds the bf16 weights as fp32. */
+void orc_quantize_weight_rows(const float* w, int64_t n, int64_t k, int8_t* q, float* s) {
+  for (int64_t r = 0; r < n; ++r) {
+    const float* row = w + r * k;
+    float mx = 0.f;
+    for (int64_t c = 0; c < k; ++c) mx = fmaxf(mx, fabsf(row[c]));
+    const float sc = fmaxf(mx, 1e-12f) / 127.f;
+    s[r] = sc;
+    for (int64_t c = 0; c < k; ++c) {
+      float v = rintf(row[c] / sc);
+      v = fminf(fmaxf(v, -127.f), 127.f);
+      q[r * k + c] = (int8_t)v;
+    }
+  }
+}
+
+/* a2: kernels/csrc/encoder_ops.cu:18-42 store_q8 (used by quantize_rows 45-54, layernorm_q8 57-79):
+ * mx = max|x| over the bf16 row; s = mx > 0 ? mx / 127 : 1; inv = 1 / s; q = rint_half_even(clamp(x * inv, +-127)). */
+void orc_q8_rows(const uint16_t* x, int64_t ldx, int64_t rows, int64_t cols, int8_t* q, int64_t ldq, float* s) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const uint16_t* row = x + r * ldx;
+    float mx = 0.f;
+    for (int64_t c = 0; c < cols; ++c) mx = fmaxf(mx, fabsf(bf2f(row[c])));
+    const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+    s[r] = sc;
+    for (int64_t c = 0; c < cols; ++c) {
+      const float v = fminf(fmaxf(bf2f(row[c]) * inv, -127.f), 127.f);
+      q[r * ldq + c] = (int8_t)rintf(v);
+    }
+  }
+}
+
+/* int32 dot product of two int8 rows (exact) */
+static inline int32_t dot_i8(const int8_t* a, const int8_t* b, int64_t k) {
+  int32_t acc = 0;
+  for (int64_t i = 0; i < k; ++i) acc += (int32_t)a[i] * (int32_t)b[i];
+  return acc;
+}
+
+/* a3, a4, a5: kernels/csrc/gemm_int8.cu:146-163 (grouped fold), 201-288 (epilogues).
+ *   acc_g = sum over K-group g of A[m,k] W[n,k] (int32, exact)
+ *   per-row scales (group == K):  x = fmul((float)acc, sa[m])
+ *   grouped (group < K):          x = fmaf((float)acc_g, sa[m,g], x) over g in order, from 0
+ *   v = bias ? fmaf(x, sw[n], bias[n]) : fmul(x, sw[n])
+ *   EPI_BIAS     out = bf16(v)
+ *   EPI_RESID    out = bf16(fmaf(alpha, bf16(v), resid))            (out may alias resid)
+ *   EPI_GLU      out[:, j] = bf16(bf16(v[2j]) * sigmoid(bf16(v[2j+1])))
+ *   EPI_SILU_Q8  u = bf16(t * sigmoid(t)), t = bf16(v); int8 per (row, qgroup columns) as store_q8, scale to qs
+ *   EPI_I32      out = acc (int32; per-row scales only; a parity hook with no counterpart in the reference)
+ * acc_out (optional, M x N int32, per-row scales only) receives the raw accumulators. */
+int orc_gemm_i8(const int8_t* a, int64_t lda, const float* sa, int64_t ldsa, int64_t group, const int8_t* w,
+                int64_t ldw, const float* sw, const uint16_t* bias, void* out, int64_t ldc, int epi,
+                const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t qgroup, int64_t M,
+                int64_t N, int64_t K, int32_t* acc_out, int nthreads) {
+  if (group <= 0 || K % group != 0) return -1;
+  if (epi == EPI_SILU_Q8 && (qgroup <= 0 || N % qgroup != 0)) return -2;
+  if (epi == EPI_GLU && N % 2 != 0) return -3;
+  const int grouped = group < K;
+  if (grouped && (epi == EPI_I32 || acc_out)) return -4;
+  const int64_t G = K / group;
+  set_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 4)
+  for (int64_t m = 0; m < M; ++m) {
+    float* v = (float*)malloc(sizeof(float) * (size_t)N);
+    const int8_t* arow = a + m * lda;
+    for (int64_t n = 0; n < N; ++n) {
+      const int8_t* wrow = w + n * ldw;
+      float x;
+      if (!grouped) {
+        const int32_t acc = dot_i8(arow, wrow, K);
+        if (acc_out) acc_out[m * N + n] = acc;
+        if (epi == EPI_I32) {
+          ((int32_t*)out)[m * ldc + n] = acc;
+          continue;
+        }
+        x = (float)acc * sa[m * ldsa];
+      } else {
+        x = 0.f;
+        for (int64_t g = 0; g < G; ++g) {
+          const int32_t acc = dot_i8(arow + g * group, wrow + g * group, group);
+          x = fmaf((float)acc, sa[m * ldsa + g], x);
+        }
+      }
+      v[n] = bias ? fmaf(x, sw[n], bf2f(bias[n])) : x * sw[n];
+    }
+    if (epi == EPI_BIAS) {
+      uint16_t* o = (uint16_t*)out + m * ldc;
+      for (int64_t n = 0; n < N; ++n) o[n] = f2bf(v[n]);
+    } else if (epi == EPI_RESID) {
+      uint16_t* o = (uint16_t*)out + m * ldc;
+      const uint16_t* r = resid + m * ldr;
+      for (int64_t n = 0; n < N; ++n) o[n] = f2bf(fmaf(alpha, round_bf(v[n]), bf2f(r[n])));
+    } else if (epi == EPI_GLU) {
+      uint16_t* o = (uint16_t*)out + m * ldc;
+      for (int64_t j = 0; j < N / 2; ++j) o[j] = f2bf(round_bf(v[2 * j]) * sigmoid(round_bf(v[2 * j + 1])));
+    } else if (epi == EPI_SILU_Q8) {
+      int8_t* o = (int8_t*)out + m * ldc;
+      for (int64_t n = 0; n < N; ++n) {
+        const float t = round_bf(v[n]);
+        v[n] = round_bf(t * sigmoid(t));
+      }
+      for (int64_t g0 = 0; g0 < N; g0 += qgroup) {
+        float mx = 0.f;
+        for (int64_t n = g0; n < g0 + qgroup; ++n) mx = fmaxf(mx, fabsf(v[n]));
+        const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+        qs[m * ldqs + g0 / qgroup] = sc;
+        for (int64_t n = g0; n < g0 + qgroup; ++n) o[n] = (int8_t)rintf(fminf(fmaxf(v[n] * inv, -127.f), 127.f));
+      }
+    }
+    free(v);
+  }
+  return 0;
+}
+
+/* a6: kernels/sparse.py:26-39 compress_24. Per group of 4 along K: the positions to keep are the nonzero ones in
+ * increasing order, then zero ones in increasing order, the first two of that list, sorted; kept values in that order;
+ * selector nibble = i0 | i1 << 2, eight nibbles per int32 word, the lowest group in the lowest nibble.
+ * Returns -1 when K % 32 != 0, -2 when a group has more than two nonzero values. */
+int orc_compress_24(const int8_t* w, int64_t n, int64_t k, int8_t* kept, int32_t* words) {
+  if (k % 32 != 0) return -1;
+  for (int64_t r = 0; r < n; ++r) {
+    for (int64_t wd = 0; wd < k / 32; ++wd) {
+      uint32_t word = 0;
+      for (int gi = 0; gi < 8; ++gi) {
+        const int8_t* g = w + r * k + wd * 32 + gi * 4;
+        int order[4], cnt = 0, nnz = 0;
+        for (int p = 0; p < 4; ++p)
+          if (g[p] != 0) order[cnt++] = p, ++nnz;
+        if (nnz > 2) return -2;
+        for (int p = 0; p < 4; ++p)
+          if (g[p] == 0) order[cnt++] = p;
+        int i0 = order[0], i1 = order[1];
+        if (i0 > i1) {
+          const int t = i0;
+          i0 = i1;
+          i1 = t;
+        }
+        const int64_t kp = r * (k / 2) + wd * 16 + gi * 2;
+        kept[kp] = g[i0];
+        kept[kp + 1] = g[i1];
+        word |= (uint32_t)(i0 | (i1 << 2)) << (4 * gi);
+      }
+      words[r * (k / 32) + wd] = (int32_t)word;
+    }
+  }
+  return 0;
+}
+
+/* inverse of compress_24: the dense (n, k) int8 matrix the compressed form stands for */
+void orc_decompress_24(const int8_t* kept, const int32_t* words, int64_t n, int64_t k, int8_t* w) {
+  memset(w, 0, (size_t)(n * k));
+  for (int64_t r = 0; r < n; ++r)
+    for (int64_t g = 0; g < k / 4; ++g) {
+      const uint32_t word = (uint32_t)words[r * (k / 32) + g / 8];
+      const int nib = (word >> (4 * (g % 8))) & 15;
+      const int i0 = nib & 3, i1 = nib >> 2;
+      w[r * k + 4 * g + i0] += kept[r * (k / 2) + 2 * g];
+      w[r * k + 4 * g + i1] += kept[r * (k / 2) + 2 * g + 1];
+    }
+}
+
+/* a7: kernels/sparse.py:42-46 prune_24_magnitude: the two smallest |w| of every group of four along K set to zero.
+ * torch.topk leaves the order of equal magnitudes unspecified; here, of equal magnitudes, the higher index is zeroed
+ * first (the lowest index is kept). */
+void orc_prune_24(const float* w, int64_t n, int64_t k, float* out) {
+  for (int64_t i = 0; i < n * k; i += 4) {
+    int idx[4] = {0, 1, 2, 3};
+    for (int a = 0; a < 4; ++a)
+      for (int b = a + 1; b < 4; ++b) {
+        const float fa = fabsf(w[i + idx[a]]), fb = fabsf(w[i + idx[b]]);
+        /* ascending magnitude; of equal magnitudes the higher index first */
+        if (fb < fa || (fb == fa && idx[b] > idx[a])) {
+          const int t = idx[a];
+          idx[a] = idx[b];
+          idx[b] = t;
+        }
+      }
+    for (int p = 0; p < 4; ++p) out[i + p] = w[i + p];
+    out[i + idx[0]] = 0.f;
+    out[i + idx[1]] = 0.f;
+  }
+}
+
+/* a10: kernels/stream_decoder.py:38-48 prepare_w8: per output channel s = max(amax|w|, 1e-12) / 127,
+ * u8 = clamp(round_half_even(w / s), +-127) + 128, the bytes of every 16 along K permuted by W8_PERM (physical
+ * position j holds logical k = PERM[j]). */
+static const int W8_PERM[16] = {0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15};
+
+void orc_prepare_w8(const float* w, int64_t n, int64_t k, uint8_t* q, float* s) {
+  for (int64_t r = 0; r < n; ++r) {
+    const float* row = w + r * k;
+    float mx = 0.f;
+    for (int64_t c = 0; c < k; ++c) mx = fmaxf(mx, fabsf(row[c]));
+    const float sc = fmaxf(mx, 1e-12f) / 127.f;
+    s[r] = sc;
+    for (int64_t b = 0; b < k; b += 16)
+      for (int j = 0; j < 16; ++j) {
+        float v = rintf(row[b + W8_PERM[j]] / sc);
+        v = fminf(fmaxf(v, -127.f), 127.f) + 128.f;
+        q[r * k + b + j] = (uint8_t)v;
+      }
+  }
+}
+
+/* a11: kernels/csrc/dec_w8.cu:46-180 dec_w8_linear: y = bf16(acc * sw[n] + bias[n]) (ReLU), acc the sum of the exact
+ * products bf16(x) * (u8 - 128). The kernel sums in fp32 in its own order; here in fp64, rounded to fp32 once. */
+void orc_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* sw, const uint16_t* bias,
+                       uint16_t* y, int64_t ldy, int relu, int64_t M, int64_t N, int64_t K, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n) {
+    for (int64_t m = 0; m < M; ++m) {
+      double acc = 0.0;
+      for (int64_t b = 0; b < K; b += 16)
+        for (int j = 0; j < 16; ++j)
+          acc += (double)bf2f(x[m * ldx + b + W8_PERM[j]]) * (double)((int)w[n * K + b + j] - 128);
+      float v = fmaf((float)acc, sw[n], bias ? bf2f(bias[n]) : 0.f);
+      if (relu) v = fmaxf(v, 0.f);
+      y[m * ldy + n] = f2bf(v);
+    }
+  }
+}
+
+/* a12: kernels/decoder_kernels.py:19-34 (and F.linear above 32 rows): y = bf16(x W^T + bias) (ReLU), fp32
+ * accumulation of bf16 products (here fp64, rounded to fp32 once), the bias added before the single rounding. */
+void orc_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
+                     int64_t ldy, int relu, int64_t M, int64_t N, int64_t K, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t m = 0; m < M; ++m) {
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k) acc += (double)bf2f(x[m * ldx + k]) * (double)bf2f(w[n * K + k]);
+      float v = (float)(acc + (bias ? (double)bf2f(bias[n]) : 0.0));
+      if (relu) v = fmaxf(v, 0.f);
+      y[m * ldy + n] = f2bf(v);
+    }
+}
+
+/* bf16 <-> fp32 helpers exported for the Python side of the checker */
+void orc_f32_to_bf16(const float* f, uint16_t* h, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) h[i] = f2bf(f[i]);
+}
+void orc_bf16_to_f32(const uint16_t* h, float* f, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) f[i] = bf2f(h[i]);
+}
