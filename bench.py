@@ -1,0 +1,327 @@
+"""Benchmark of the MI355X quantized-GEMM hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only dominant|step]
+
+Workload (the metric's configuration): one step = the 2:4-sparse W8A8 linear at
+M=3000 (8 clips x 375 frames), N=5120, K=1280 with bias, followed by the down projection M=3000, N=1280, K=5120
+(per-row activation scales, bias), on resident synthetic inputs (seeded N(0,1) activations quantized per row on the
+GPU; N(0,0.02) weights pruned 2:4 by magnitude, quantized per channel, compressed). value = dense-equivalent int8
+ops (2*M*N*K per GEMM) per second over the whole step, in TOPS.
+
+Timing: steps are captured into a HIP graph (torch.cuda.CUDAGraph; the kernels are launched on the current stream
+through the C ABI) and replayed; W warm-up steps, then exactly K timed steps between synchronizations, timed with HIP
+events on the launching stream. The roofline figure is the dominant kernel's: its own graph of back-to-back launches,
+timed with HIP events, priced against MI355X's sparse int8 peak (10.1 POPS dense-equivalent, i.e. 5.0 POPS of
+executed MFMA work). The CPU baseline is the oracle's C restatement (OpenMP, all host threads) on a bounded sample of
+the same workload (dense on the pruned weights, as the CPU has no 2:4 path), next to the reference's CPU path
+(torch._int_mm) on the same sample.
+
+Extras (not the metric): config 0 (dense W8A8 5120x1280, bias) TOPS against the dense peak, and config 3's decoder-
+step projections (M=64, 8 layers + head, all int8 weights) in GB/s against 8 TB/s, cold-cache (weight sets rotated so
+the 256 MB Infinity Cache cannot hold them).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "cohere-inference_amd"))
+
+PEAK_INT8_DENSE = 5.0e15
+PEAK_INT8_SPARSE = 10.1e15  # dense-equivalent ops/s of 2:4 SMFMAC
+PEAK_HBM = 8.0e12
+M, D, F = 3000, 1280, 5120
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder"], default=None,
+                    help="run one part only (for rocprofv3 runs)")
+    ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
+    return ap.parse_args()
+
+
+def draw_config1(dev):
+    """Seeded config-1 inputs on the GPU (seed 0: X, W, bias of the up projection, then those of the down one)."""
+    import torch
+
+    from kernels.fast_encoder import Int8Linear, quantize_activations
+
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, D, generator=g).to(torch.bfloat16)
+    w_up = (torch.randn(F, D, generator=g) * 0.02).to(torch.bfloat16)
+    b_up = (torch.randn(F, generator=g) * 0.01).to(torch.bfloat16)
+    xd = torch.randn(M, F, generator=g).to(torch.bfloat16)
+    w_dn = (torch.randn(D, F, generator=g) * 0.02).to(torch.bfloat16)
+    b_dn = (torch.randn(D, generator=g) * 0.01).to(torch.bfloat16)
+    up_s = Int8Linear(w_up, b_up, sparse=True)
+    dn_s = Int8Linear(w_dn, b_dn, sparse=True)
+    up_d = Int8Linear(w_up, b_up, sparse=False)
+    for lin in (up_s, dn_s, up_d):
+        for name in ("q", "s", "bias", "wc", "e"):
+            if hasattr(lin, name) and getattr(lin, name) is not None:
+                setattr(lin, name, getattr(lin, name).to(dev))
+    xq, xs = quantize_activations(x.to(dev))
+    xdq, xds = quantize_activations(xd.to(dev))
+    return dict(xq=xq, xs=xs, xdq=xdq, xds=xds, up_s=up_s, dn_s=dn_s, up_d=up_d)
+
+
+def graph_of(fn, reps):
+    """A HIP graph of `reps` back-to-back calls of fn (captured on a side stream, as torch requires)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    return g
+
+
+def time_graph(g, replays):
+    """Average ms per replay over `replays`, HIP events on the current (launching) stream."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / replays
+
+
+def cpu_baseline(target_s=10.0):
+    """The oracle (C, OpenMP over all host threads) on full config-1 steps, dense on the pruned weights, repeated
+    until target_s; plus torch._int_mm (the reference's CPU int8 path) on one step."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    threads = os.cpu_count() or 1
+    rng = np.random.default_rng(0)
+    xq = rng.integers(-127, 128, (M, D)).astype(np.int8)
+    xs = np.full(M, 0.01, np.float32)
+    xdq = rng.integers(-127, 128, (M, F)).astype(np.int8)
+    w_up = rng.integers(-127, 128, (F, D)).astype(np.int8)
+    w_dn = rng.integers(-127, 128, (D, F)).astype(np.int8)
+    for w in (w_up, w_dn):  # 2:4 pattern: dense on pruned
+        w.reshape(w.shape[0], -1, 4)[..., 2:] = 0
+    s_up, s_dn = np.full(F, 1e-3, np.float32), np.full(D, 1e-3, np.float32)
+    b_up = np.zeros(F, np.uint16)
+    b_dn = np.zeros(D, np.uint16)
+    ops = 2.0 * M * F * D * 2
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        O.gemm_i8(xq, xs, D, w_up, s_up, b_up, O.EPI_BIAS, threads=threads)
+        O.gemm_i8(xdq, xs, F, w_dn, s_dn, b_dn, O.EPI_BIAS, threads=threads)
+        steps += 1
+        if time.perf_counter() - t0 >= target_s:
+            break
+    dt = (time.perf_counter() - t0) / steps
+    torch.set_num_threads(threads)
+    a1, a2 = torch.from_numpy(xq), torch.from_numpy(xdq)
+    b1, b2 = torch.from_numpy(w_up).t().contiguous(), torch.from_numpy(w_dn).t().contiguous()
+    best = 1e9
+    for _ in range(3):
+        t = time.perf_counter()
+        torch._int_mm(a1, b1)
+        torch._int_mm(a2, b2)
+        best = min(best, time.perf_counter() - t)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{steps} full config-1 steps (3000x5120x1280 + 3000x1280x5120, dense on 2:4-pruned int8 "
+                      f"weights, bias epilogue) in {dt * steps:.1f} s, oracle/cohere_oracle.c",
+            "cpu_model": model,
+            "reference_cpu_path_int_mm": {"value": round(ops / best / 1e12, 4), "unit": "TOPS", "threads": threads,
+                                          "what": "torch._int_mm on the same step, int32 result only, best of 3"}}
+
+
+def decoder_extra(dev, reps_sets=4):
+    """Config 3's step projections at M=64 (8 layers x qkv/o/cq/co/fc1/fc2 + head, all int8 weights), cold cache:
+    reps_sets copies of the weights (> 512 MB) rotated step to step."""
+    import torch
+
+    from kernels.cuda_ext import ext
+
+    shapes = [(3072, 1024, False), (1024, 1024, False), (1024, 1024, False), (1024, 1024, False),
+              (4096, 1024, True), (1024, 4096, False)]
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(64, 4096, generator=g).to(torch.bfloat16).to(dev)
+    ys = torch.empty(64, 16384, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(8 << 20, dtype=torch.float32, device=dev)
+    counters = torch.zeros(1024, dtype=torch.int32, device=dev)
+    sets = []
+    for _ in range(reps_sets):
+        layers = []
+        for _l in range(8):
+            for n, k, relu in shapes:
+                w = torch.randint(0, 256, (n, k), dtype=torch.uint8, device=dev)
+                layers.append((w, torch.rand(n, device=dev) * 1e-3, torch.zeros(n, dtype=torch.bfloat16, device=dev),
+                               relu))
+        layers.append((torch.randint(0, 256, (16384, 1024), dtype=torch.uint8, device=dev),
+                       torch.rand(16384, device=dev) * 1e-3, torch.zeros(16384, dtype=torch.bfloat16, device=dev),
+                       False))
+        sets.append(layers)
+    bytes_step = sum(w.numel() + 6 * w.shape[0] + 2 * 64 * (w.shape[1] + w.shape[0]) for w, _, _, _ in sets[0])
+
+    def step(layers):
+        for w, s, b, relu in layers:
+            n, k = w.shape
+            ext.dec_w8_linear(x[:, :k], w, s, b, ys[:, :n], relu, 64, 4 if k % 512 == 0 else 1, ws, counters)
+
+    graphs = [graph_of(lambda L=L: step(L), 1) for L in sets]
+    for gr in graphs:
+        gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    rounds = 25
+    e0.record()
+    for _ in range(rounds):
+        for gr in graphs:
+            gr.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (rounds * len(graphs))
+    return {"what": "config-3 decoder step projections, M=64, 8 layers x (qkv 3072x1024, o/cq/co 1024x1024, "
+                    "fc1 4096x1024 relu, fc2 1024x4096) + head 16384x1024, all int8 weights (W8A16), cold cache "
+                    f"({reps_sets} weight sets rotated, {reps_sets * bytes_step / 1e6:.0f} MB)",
+            "launches_per_step": len(sets[0]), "ms_per_step": round(ms, 4),
+            "bytes_per_step": bytes_step, "GBps": round(bytes_step / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm": round(bytes_step / (ms * 1e-3) / PEAK_HBM, 4)}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards by data "
+              "parallelism with no exchange (see DESIGN.md), and no multi-GPU figure is produced.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from kernels.cuda_ext import ext
+
+    dev = torch.device("cuda:0")
+    ext.set_gemm_tile(args.tile)
+    d = draw_config1(dev)
+    up_out = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
+    dn_out = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    from kernels.cuda_ext import EPI_BIAS
+
+    def up():
+        d["up_s"](d["xq"], d["xs"], EPI_BIAS, out=up_out)
+
+    def down():
+        d["dn_s"](d["xdq"], d["xds"], EPI_BIAS, out=dn_out)
+
+    def step():
+        up()
+        down()
+
+    ops_up = 2.0 * M * F * D
+    ops_dn = 2.0 * M * D * F
+    ops_step = ops_up + ops_dn
+    result = {}
+
+    if args.only in (None, "step"):
+        per_graph = 10
+        g = graph_of(step, per_graph)
+        g1 = graph_of(step, 1)
+        for _ in range(max(1, args.warmup // per_graph)):
+            g.replay()
+        for _ in range(args.warmup % per_graph):
+            g1.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_host = time.perf_counter()
+        e0.record()
+        for _ in range(args.steps // per_graph):
+            g.replay()
+        for _ in range(args.steps % per_graph):
+            g1.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        t_host = time.perf_counter() - t_host
+        ms = e0.elapsed_time(e1) / args.steps
+        result.update(ms_per_step=ms, host_ms_per_step=t_host * 1e3 / args.steps)
+
+    if args.only in (None, "dominant"):
+        # each kernel of the step alone: the dominant one's duration prices the roofline
+        reps = 20
+        ms_up = time_graph(graph_of(up, reps), 10) / reps
+        ms_dn = time_graph(graph_of(down, reps), 10) / reps
+        dom = ("gemm_sp up 3000x5120x1280", ms_up, ops_up) if ms_up >= ms_dn else \
+              ("gemm_sp down 3000x1280x5120", ms_dn, ops_dn)
+        achieved = dom[2] / (dom[1] * 1e-3)
+        result["roofline"] = {"kernel": f"gemm_q8_kernel (2:4 sparse, {dom[0]})", "bound": "mfma",
+                              "achieved": round(achieved / 1e12, 2), "peak": PEAK_INT8_SPARSE / 1e12,
+                              "unit": "TFLOP/s", "frac": round(achieved / PEAK_INT8_SPARSE, 4), "traffic": None,
+                              "ops_per_launch": dom[2], "ms_per_launch": round(dom[1], 5),
+                              "note": "int8 TOPS, dense-equivalent (2*M*N*K) against the 2:4 SMFMAC peak"}
+        result["kernels_ms"] = {"sparse_up": round(ms_up, 5), "sparse_down": round(ms_dn, 5)}
+
+    if not args.no_extras and args.only in (None, "dense"):
+        def dense():
+            d["up_d"](d["xq"], d["xs"], EPI_BIAS, out=up_out)
+
+        ms_d = time_graph(graph_of(dense, 20), 10) / 20
+        result["dense_config0"] = {"what": "dense W8A8 3000x5120x1280, bias epilogue (config 0)",
+                                   "ms": round(ms_d, 5), "TOPS": round(ops_up / (ms_d * 1e-3) / 1e12, 1),
+                                   "frac_of_dense_peak": round(ops_up / (ms_d * 1e-3) / PEAK_INT8_DENSE, 4)}
+    if not args.no_extras and args.only in (None, "decoder"):
+        result["decoder_gemms"] = decoder_extra(dev)
+
+    if args.only is not None:
+        print(json.dumps(result))
+        return
+
+    line = {
+        "metric": "int8 & 2:4 GEMM TOPS (% of peak); encoder+decode audio-sec/sec, 1 GPU",
+        "value": round(ops_step / (result["ms_per_step"] * 1e-3) / 1e12, 2),
+        "unit": "TOPS (dense-equivalent int8 ops/s)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(result["ms_per_step"], 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights pruned 2:4, random init)",
+        "config": {"workload": "config 1: 2:4-sparse W8A8 linear 3000x5120x1280 (bias) + down projection "
+                               "3000x1280x5120 (per-row scales, bias), one step = both GEMMs",
+                   "M": M, "shapes": [[M, F, D], [M, D, F]], "parallelism": "none (1 GPU)"},
+        "roofline": result["roofline"],
+        "kernels_ms": result["kernels_ms"],
+    }
+    line["frac_of_sparse_peak"] = round(line["value"] * 1e12 / PEAK_INT8_SPARSE, 4)
+    for k in ("dense_config0", "decoder_gemms"):
+        if k in result:
+            line[k] = result[k]
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -148,19 +148,22 @@ bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 extern "C" int cohere_quantize_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int64_t rows,
                                     int64_t cols, void* stream) {
   cohere::clear_error();
-  COHERE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 2048,
-                 "quantize_rows: cols must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 8192,
+                 "quantize_rows: cols must be a multiple of 8, at most 8192");
   COHERE_REQUIRE(x && q && s && al16(x) && ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 7) == 0 && ldq % 8 == 0,
                  "quantize_rows: rows must be aligned");
   if (rows == 0) return 0;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int grid = (int)((rows + 3) / 4), vec = (int)((cols + 511) / 512);
-  switch (vec) {
-    case 1: quantize_rows_kernel<1><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
-    case 2: quantize_rows_kernel<2><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
-    case 3: quantize_rows_kernel<3><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
-    default: quantize_rows_kernel<4><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols); break;
-  }
+#define QR(V) quantize_rows_kernel<V><<<grid, 256, 0, st>>>(x, ldx, q, ldq, s, (int)rows, (int)cols)
+  if (vec <= 1) QR(1);
+  else if (vec <= 2) QR(2);
+  else if (vec <= 3) QR(3);
+  else if (vec <= 4) QR(4);
+  else if (vec <= 8) QR(8);
+  else if (vec <= 10) QR(10);
+  else QR(16);
+#undef QR
   return cohere::check_launch("quantize_rows");
 }
 

@@ -62,7 +62,8 @@ int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, 
                    int64_t K, int32_t cfg, void* stream);
 
 /* Replaces quantize_rows (reference kernels/csrc/encoder_ops.cu:545-553, bound at bindings.cpp:70): bf16 rows x
- * [rows, cols] (ldx) -> int8 q [rows, cols] (ldq) and fp32 s [rows]; one scale per row, absmax / 127. */
+ * [rows, cols] (ldx) -> int8 q [rows, cols] (ldq) and fp32 s [rows]; one scale per row, absmax / 127;
+ * cols % 8 == 0, cols <= 8192. */
 int cohere_quantize_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int64_t rows, int64_t cols,
                          void* stream);
 

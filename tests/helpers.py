@@ -35,3 +35,24 @@ def rel_err(got: np.ndarray, want: np.ndarray) -> float:
     got, want = got.astype(np.float64), want.astype(np.float64)
     rms = np.sqrt(np.mean(want ** 2)) + 1e-30
     return float(np.max(np.abs(got - want)) / rms) if got.size else 0.0
+
+
+def bf16_ulp(v: np.ndarray) -> np.ndarray:
+    """The bf16 ulp at |v| (8 significant bits)."""
+    a = np.abs(v.astype(np.float64))
+    e = np.floor(np.log2(np.where(a > 0, a, 1e-38)))
+    return np.where(a > 0, 2.0 ** (e - 7), 2.0 ** -133)
+
+
+def assert_bf16_close(got_bits: np.ndarray, want_bits: np.ndarray, max_frac: float = 0.01) -> None:
+    """The numeric bar for bf16 outputs computed with a different fp32 summation order than the checker: every
+    element within max-abs 1e-2 x RMS of the checker's, except where one bf16 ulp of the value itself is larger than
+    that (a rounding flip at |v| > ~2.5 RMS), which may differ by that one ulp; and at most max_frac of the elements
+    differ at all."""
+    got, want = bf16_float(got_bits).astype(np.float64), bf16_float(want_bits).astype(np.float64)
+    rms = np.sqrt(np.mean(want ** 2))
+    tol = np.maximum(1e-2 * rms, bf16_ulp(want) * 1.0001)
+    diff = np.abs(got - want)
+    bad = diff > tol
+    assert not bad.any(), f"{int(bad.sum())} elements beyond tolerance, worst {float((diff / tol).max()):.3f} x tol"
+    assert (got_bits != want_bits).mean() <= max_frac, f"{(got_bits != want_bits).mean():.4f} of elements differ"

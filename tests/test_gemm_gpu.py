@@ -12,7 +12,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import bf16_bits, bf16_float, linear_inputs, rel_err
+from helpers import assert_bf16_close, bf16_bits, bf16_float, linear_inputs, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -134,11 +134,8 @@ def test_gemm_glu(ext):
     _, xq, xs, wq, ws, b = _prep(M, N, K, seed=6)
     out = torch.empty(M, N // 2, dtype=torch.bfloat16, device="cuda")
     ext.gemm_i8(xq, xs, K, wq, ws, b, out, EPI_GLU, None, 1.0, None, 0)
-    want = bf16_float(O.gemm_i8(_np(xq), _np(xs), K, _np(wq), _np(ws), bf16_bits(b), O.EPI_GLU))
-    got = bf16_float(bf16_bits(out))
-    assert rel_err(got, want) <= 1e-2
-    assert (np.abs(got - want) <= np.abs(want) * 2.0 ** -7 + 1e-30).all()  # one bf16 ulp (sigmoid's exp)
-    assert (got != want).mean() < 1e-2
+    want = O.gemm_i8(_np(xq), _np(xs), K, _np(wq), _np(ws), bf16_bits(b), O.EPI_GLU)
+    assert_bf16_close(bf16_bits(out), want)  # the sigmoid's exp differs from libm's: rare one-ulp flips
 
 
 @pytest.mark.parametrize("cfg,group", [(4, 256), (0, 128), (5, 64), (-1, 256)])
