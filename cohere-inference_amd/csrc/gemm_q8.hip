@@ -59,7 +59,7 @@ struct GemmArgs {
   float alpha;
 };
 
-template <int BM, int BN, int WM, int WN, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, bool GROUPED, bool SPARSE>
 struct Tile {
   static constexpr int NW = WM * WN, NT = NW * 64;
   static constexpr int TM = BM / WM, TN = BN / WN, MI = TM / 16, NI = TN / 16;
@@ -67,16 +67,42 @@ struct Tile {
   static constexpr int W_STAGE = SPARSE ? BN * 64 : BN * 128;
   static constexpr int E_STAGE = SPARSE ? BN * 16 : 0;
   static constexpr int STAGE = X_STAGE + W_STAGE + E_STAGE;
-  static constexpr int PIPE = 2 * STAGE;
+  static constexpr int PIPE = ST * STAGE;
+  static constexpr int GFIT = (160 * 1024 - PIPE) / (BM * 4);
+  static constexpr int GMAX = GFIT < 32 ? GFIT : 32;  // K-groups whose token scales are kept in LDS
+  static constexpr int SCALES = GROUPED ? GMAX * BM * 4 : 0;
   static constexpr int LDC = BN + 8;  // staged output row (bf16 elements)
   static constexpr int OUTB = BM * LDC * 2;
-  static constexpr int SMEM = PIPE > OUTB ? PIPE : OUTB;
-  static constexpr int KSTEP = SPARSE ? 128 : 64;  // K per matrix instruction
-  static_assert(TM % 16 == 0 && TN % 16 == 0 && BM % 8 == 0, "tile shape");
+  static constexpr int SMEM = (PIPE + SCALES) > OUTB ? (PIPE + SCALES) : OUTB;
+  // 1 KB DMA instructions per stage: tokens (8 rows each), weights (8 dense rows / 16 compressed rows), selectors
+  // (one per wave, BN/NW rows)
+  static constexpr int X_SLOTS = BM / 8, W_SLOTS = SPARSE ? BN / 16 : BN / 8;
+  static constexpr int LPS = X_SLOTS / NW + W_SLOTS / NW + (SPARSE ? 1 : 0);  // per wave per stage
+  static_assert(TM % 16 == 0 && TN % 16 == 0, "tile shape");
+  static_assert(X_SLOTS % NW == 0 && W_SLOTS % NW == 0 && BN / NW <= 64, "DMA slots must split evenly over waves");
+  static_assert(LPS * (ST - 2 > 0 ? ST - 2 : 0) <= 63, "vmcnt range");
+  static_assert(PIPE + SCALES <= 160 * 1024, "LDS");
 };
 
 DEVI void dma16(const void* g, char* lds_slot) {
   __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds_slot, 16, 0, 0);
+}
+
+template <int N>
+DEVI void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait until at most `after` stages of this wave's DMA (LPS instructions each) are still in flight
+template <int LPS, int ST>
+DEVI void wait_stages(int after) {
+  if constexpr (ST >= 4) {
+    if (after >= 2) { wait_vm<2 * LPS>(); return; }
+  }
+  if constexpr (ST >= 3) {
+    if (after >= 1) { wait_vm<LPS>(); return; }
+  }
+  wait_vm<0>();
 }
 
 // 16-byte chunk `c` (0..7) of row `r` of a 128-byte-row tile
@@ -84,10 +110,10 @@ DEVI int sw128(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 // chunk `c` (0..3) of row `r` of a 64-byte-row tile
 DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
-template <int BM, int BN, int WM, int WN, bool GROUPED, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, bool GROUPED, bool SPARSE>
 __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) {
-  using T = Tile<BM, BN, WM, WN, SPARSE>;
-  constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI;
+  using T = Tile<BM, BN, WM, WN, ST, GROUPED, SPARSE>;
+  constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI, LPS = T::LPS;
   __shared__ __attribute__((aligned(16))) char smem[T::SMEM];
 
   const int M = p.M, N = p.N, K = p.K;
@@ -107,38 +133,51 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   const int KT = (K + 127) / 128;
   const bool half_last = (K & 127) != 0;  // dense only: the last tile holds 64 K
 
+  // grouped: every group's token scales of this tile in LDS, loaded before the first DMA (read after a barrier)
+  float* sS = reinterpret_cast<float*>(smem + T::PIPE);
+  const int G = GROUPED ? K / (p.group_steps * (SPARSE ? 128 : 64)) : 1;
+  const bool scales_in_lds = GROUPED && G <= T::GMAX;
+  if (scales_in_lds) {
+    for (int i = tid; i < G * BM; i += NT) {
+      const int g = i / BM, r = i % BM;
+      sS[i] = p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+    }
+  }
+
   auto issue = [&](int buf, int kt) {
     char* base = smem + buf * T::STAGE;
     const bool half = half_last && kt == KT - 1;
     const int64_t k0 = (int64_t)kt * 128;
-    // tokens: 8 rows of 128 B per DMA instruction
-    for (int s = wave; s < BM / 8; s += NW) {
-      const int r = s * 8 + (lane >> 3), pc = lane & 7;
-      int lc = pc ^ (r & 7);
+#pragma unroll
+    for (int j = 0; j < T::X_SLOTS / NW; ++j) {  // tokens: 8 rows of 128 B per instruction
+      const int s = wave + j * NW;
+      const int r = s * 8 + (lane >> 3);
+      int lc = (lane & 7) ^ (r & 7);
       if (half) lc &= 3;
-      const int gm = min(m0 + r, M - 1);
-      dma16(p.X + (int64_t)gm * p.ldx + k0 + lc * 16, base + s * 1024);
+      dma16(p.X + (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + lc * 16, base + s * 1024);
     }
     char* wbase = base + T::X_STAGE;
     if constexpr (!SPARSE) {
-      for (int s = wave; s < BN / 8; s += NW) {
-        const int r = s * 8 + (lane >> 3), pc = lane & 7;
-        int lc = pc ^ (r & 7);
+#pragma unroll
+      for (int j = 0; j < T::W_SLOTS / NW; ++j) {
+        const int s = wave + j * NW;
+        const int r = s * 8 + (lane >> 3);
+        int lc = (lane & 7) ^ (r & 7);
         if (half) lc &= 3;
         dma16(p.W + (int64_t)(n0 + r) * K + k0 + lc * 16, wbase + s * 1024);
       }
     } else {
-      // kept values: 16 rows of 64 B per instruction
-      for (int s = wave; s < BN / 16; s += NW) {
-        const int r = s * 16 + (lane >> 2), pc = lane & 3, lc = pc ^ ((r >> 1) & 3);
+#pragma unroll
+      for (int j = 0; j < T::W_SLOTS / NW; ++j) {  // kept values: 16 rows of 64 B per instruction
+        const int s = wave + j * NW;
+        const int r = s * 16 + (lane >> 2), lc = (lane & 3) ^ ((r >> 1) & 3);
         dma16(p.W + (int64_t)(n0 + r) * (K / 2) + k0 / 2 + lc * 16, wbase + s * 1024);
       }
-      // selectors: 16 B (4 words) a row, 64 rows per instruction
-      char* ebase = wbase + T::W_STAGE;
-      for (int s = wave; s * 64 < BN; s += NW) {
-        const int r = s * 64 + lane;
-        if (r < BN) dma16(p.E + (int64_t)(n0 + r) * (K / 32) + k0 / 32, ebase + s * 1024);
-      }
+      // selectors: 16 B (4 words) a row; wave w brings rows [w BN/NW, (w+1) BN/NW)
+      constexpr int ER = BN / NW;
+      char* ebase = wbase + T::W_STAGE + wave * ER * 16;
+      const int r = wave * ER + lane;
+      if (lane < ER) dma16(p.E + (int64_t)(n0 + r) * (K / 32) + k0 / 32, ebase);
     }
   };
 
@@ -160,45 +199,50 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     if constexpr (GROUPED) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int m = min(m0 + wm * TM + i * 16 + (lane & 15), M - 1);
-        const float s = p.sx[(int64_t)m * p.ldsx + g];
+        const int r = wm * TM + i * 16 + (lane & 15);
+        const float s = scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) accf[j][i][r] = __builtin_fmaf((float)acc[j][i][r], s, accf[j][i][r]);
+          for (int q = 0; q < 4; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], s, accf[j][i][q]);
           acc[j][i] = v4i{0, 0, 0, 0};
         }
       }
     }
   };
 
-  issue(0, 0);
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s)
+    if (s < KT) issue(s, s);
   int kstep = 0;
   for (int kt = 0; kt < KT; ++kt) {
-    wait_vmem();
+    wait_stages<LPS, ST>(min(KT - 1 - kt, ST - 2));
     __syncthreads();
-    if (kt + 1 < KT) issue((kt + 1) & 1, kt + 1);
-    const char* xs = smem + (kt & 1) * T::STAGE;
+    if (kt + ST - 1 < KT) issue((kt + ST - 1) % ST, kt + ST - 1);
+    const char* xs = smem + (kt % ST) * T::STAGE;
     const char* ws = xs + T::X_STAGE;
     if constexpr (!SPARSE) {
-      const int steps = (half_last && kt == KT - 1) ? 1 : 2;
-      for (int s = 0; s < steps; ++s) {
-        v4i bx[MI], aw[NI];
+      const bool two = !(half_last && kt == KT - 1);
+      v4i bx[2][MI], aw[2][NI];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 1 && !two) break;
         const int lc = s * 4 + (lane >> 4);
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-          const int r = wm * TM + i * 16 + (lane & 15);
-          bx[i] = *reinterpret_cast<const v4i*>(xs + sw128(r, lc));
-        }
+        for (int i = 0; i < MI; ++i)
+          bx[s][i] = *reinterpret_cast<const v4i*>(xs + sw128(wm * TM + i * 16 + (lane & 15), lc));
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int r = wn * TN + j * 16 + (lane & 15);
-          aw[j] = *reinterpret_cast<const v4i*>(ws + sw128(r, lc));
-        }
+        for (int j = 0; j < NI; ++j)
+          aw[s][j] = *reinterpret_cast<const v4i*>(ws + sw128(wn * TN + j * 16 + (lane & 15), lc));
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 1 && !two) break;
 #pragma unroll
         for (int j = 0; j < NI; ++j)
 #pragma unroll
-          for (int i = 0; i < MI; ++i) acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw[j], bx[i], acc[j][i], 0, 0, 0);
+          for (int i = 0; i < MI; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw[s][j], bx[s][i], acc[j][i], 0, 0, 0);
         if constexpr (GROUPED) {
           ++kstep;
           if (kstep % p.group_steps == 0) fold(kstep / p.group_steps - 1);
@@ -234,7 +278,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       }
     }
   }
-  wait_vmem();
+  wait_vm<0>();
   __syncthreads();
 
   // ---- epilogue ----------------------------------------------------------------------------------------------------
@@ -366,35 +410,38 @@ struct TileInfo {
   bool grouped_ok;
 };
 
-// tile ids: 0 128x128 (2x2 waves), 1 128x256 (2x2), 2 256x128 (2x2), 3 64x128 (2x2), 4 64x256 (1x4), 5 32x128 (1x4),
-// 6 256x256 (2x4 waves), 7 64x64 (2x2)
+// tile id: tokens x channels (waves M x N, pipeline stages)
+//   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
+//   5 32x128 (1x4, 4)    6 256x256 (2x4, 2)   7 64x64 (2x2, 4)     8 256x128 (4x2, 3)  9 128x256 (2x4, 3)
 constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
-                              {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true}};
+                              {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
+                              {256, 128, true}, {128, 256, true}};
 constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
 
 int g_tile_override = -1;
 
-template <int BM, int BN, int WM, int WN, bool GROUPED, bool SPARSE>
-hipError_t launch_tile(const GemmArgs& p, hipStream_t s) {
+template <int BM, int BN, int WM, int WN, int ST, bool GROUPED, bool SPARSE>
+void launch_tile(const GemmArgs& p, hipStream_t s) {
   const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
-  gemm_q8_kernel<BM, BN, WM, WN, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
-  return hipSuccess;
+  gemm_q8_kernel<BM, BN, WM, WN, ST, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
 }
 
 template <bool GROUPED, bool SPARSE>
 int launch(int tile, const GemmArgs& p, hipStream_t s) {
   switch (tile) {
-    case 0: launch_tile<128, 128, 2, 2, GROUPED, SPARSE>(p, s); break;
-    case 3: launch_tile<64, 128, 2, 2, GROUPED, SPARSE>(p, s); break;
-    case 4: launch_tile<64, 256, 1, 4, GROUPED, SPARSE>(p, s); break;
-    case 5: launch_tile<32, 128, 1, 4, GROUPED, SPARSE>(p, s); break;
-    case 7: launch_tile<64, 64, 2, 2, GROUPED, SPARSE>(p, s); break;
+    case 0: launch_tile<128, 128, 2, 2, 4, GROUPED, SPARSE>(p, s); break;
+    case 3: launch_tile<64, 128, 2, 2, 4, GROUPED, SPARSE>(p, s); break;
+    case 4: launch_tile<64, 256, 1, 4, 3, GROUPED, SPARSE>(p, s); break;
+    case 5: launch_tile<32, 128, 1, 4, 4, GROUPED, SPARSE>(p, s); break;
+    case 7: launch_tile<64, 64, 2, 2, 4, GROUPED, SPARSE>(p, s); break;
+    case 8: launch_tile<256, 128, 4, 2, 3, GROUPED, SPARSE>(p, s); break;
+    case 9: launch_tile<128, 256, 2, 4, 3, GROUPED, SPARSE>(p, s); break;
     default:
       if constexpr (!GROUPED) {
         switch (tile) {
-          case 1: launch_tile<128, 256, 2, 2, false, SPARSE>(p, s); break;
-          case 2: launch_tile<256, 128, 2, 2, false, SPARSE>(p, s); break;
-          case 6: launch_tile<256, 256, 2, 4, false, SPARSE>(p, s); break;
+          case 1: launch_tile<128, 256, 2, 2, 3, false, SPARSE>(p, s); break;
+          case 2: launch_tile<256, 128, 2, 2, 3, false, SPARSE>(p, s); break;
+          case 6: launch_tile<256, 256, 2, 4, 2, false, SPARSE>(p, s); break;
           default: cohere::set_error("gemm: bad tile"); return 1;
         }
       } else {
@@ -416,7 +463,7 @@ int choose_tile(const GemmArgs& p, bool grouped) {
   };
   if (g_tile_override >= 0 && g_tile_override < N_TILES && fits(g_tile_override)) return g_tile_override;
   auto tiles_of = [&](int id) { return (int64_t)((p.M + TILES[id].bm - 1) / TILES[id].bm) * (p.N / TILES[id].bn); };
-  static const int order[] = {1, 2, 0, 4, 3, 5};  // preferred first
+  static const int order[] = {9, 1, 8, 2, 0, 4, 3, 5};  // preferred first
   for (int id : order)
     if (fits(id) && tiles_of(id) >= 400) return id;
   for (int id : {0, 4, 3, 5})

@@ -28,7 +28,8 @@ EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the 
 
 # every symbol include/cohere_hip.h declares
 EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_layernorm_q8", "cohere_dec_w8_linear",
-           "cohere_linear_bf16", "cohere_last_error", "cohere_version", "cohere_set_gemm_tile")
+           "cohere_linear_bf16", "cohere_last_error", "cohere_version", "cohere_set_gemm_tile",
+           "cohere_set_skinny_shape")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -45,6 +46,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_dec_w8_linear": [P, I64, P, P, P, P, I64, I32, I64, I64, P, I64, P, I64, I64, I64, I64, P],
         "cohere_linear_bf16": [P, I64, P, P, P, I64, I32, I64, I64, I64, P],
         "cohere_set_gemm_tile": [I32],
+        "cohere_set_skinny_shape": [I32, I32],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -88,6 +90,10 @@ class _Ext:
     def set_gemm_tile(self, tile: int) -> int:
         """Tuning hook: force a gfx950 GEMM tile (-1 = automatic). Results never depend on it."""
         return self._lib.cohere_set_gemm_tile(int(tile))
+
+    def set_skinny_shape(self, strips: int, waves: int) -> None:
+        """Tuning hook: force the skinny projections' workgroup shape (strips <= 0 = automatic)."""
+        self._lib.cohere_set_skinny_shape(int(strips), int(waves))
 
     # ---- int8 GEMMs (bindings.cpp:41-43, 59-61) ----------------------------------------------------------------------
 

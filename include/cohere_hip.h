@@ -77,15 +77,17 @@ int cohere_layernorm_q8(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint
 /* Replaces dec_w8_linear (reference kernels/csrc/dec_w8.cu:207-234, bound at bindings.cpp:76). y bf16 [M, N] (ldy) =
  * x bf16 [M, K] (ldx) @ dequant(w)^T + bias (ReLU), M <= 64; w uint8 [N, K] in prepare_w8's layout (int8 + 128,
  * bytes permuted within every 16 of K, reference kernels/stream_decoder.py:38-48), sw fp32 [N]. bn (16, 32, 64) and
- * splits (1..16, K % (128 * splits) == 0) are the reference's tuning knobs; splits > 1 needs ws (fp32, >= N/bn *
- * splits * 64 * bn elements) and counters (int32, >= N/bn, zero on the first call; the kernel leaves them zero). */
+ * splits (1..16, K % (128 * splits) == 0) are the reference's tuning knobs, checked as it checks them (splits > 1
+ * needs ws, fp32 >= N/bn * splits * 64 * bn elements, and counters, int32 >= N/bn); the gfx950 kernel reduces K
+ * inside each workgroup, so it chooses its own tiling and never touches ws or counters. Needs N % 16 == 0 and
+ * K % 64 == 0. */
 int cohere_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* sw, const uint16_t* bias,
                          uint16_t* y, int64_t ldy, int32_t relu, int64_t bn, int64_t splits, float* ws, int64_t ws_len,
                          int32_t* counters, int64_t counters_len, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* Replaces the bf16 decoder projections (reference kernels/decoder_kernels.py:55-66 `linear`, Triton for <= 32 rows;
  * kernels/stream_decoder.py:23-27 F.linear above): y bf16 [M, N] = x bf16 [M, K] @ w bf16 [N, K]^T + bias (ReLU),
- * M <= 64, fp32 accumulation. */
+ * M <= 64, fp32 accumulation; N % 16 == 0, K % 64 == 0. */
 int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
                        int64_t ldy, int32_t relu, int64_t M, int64_t N, int64_t K, void* stream);
 
@@ -98,6 +100,11 @@ const char* cohere_version(void);
 /* Tuning hook (no counterpart in the reference): force the gfx950 tile of the int8 GEMMs (-1 = automatic choice by
  * shape). Used by bench.py's sweeps; results never depend on it. Returns the number of tiles available. */
 int cohere_set_gemm_tile(int32_t tile);
+
+/* Tuning hook (no counterpart in the reference): force the skinny projections' workgroup shape -- strips of 16
+ * channels per workgroup (1, 2, 4) and waves per workgroup (4, 8, 16); strips <= 0 restores the automatic choice.
+ * Results never depend on it. */
+int cohere_set_skinny_shape(int32_t strips, int32_t waves);
 
 #ifdef __cplusplus
 }
