@@ -19,20 +19,20 @@ typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 
 DEVI float bf2f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// fp32 -> bf16, round to nearest even (NaN kept quiet)
-DEVI uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16, round to nearest even: gfx950's v_cvt_pk_bf16_f32
+DEVI uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 DEVI float round_bf(float f) { return bf2f(f2bf(f)); }
 
-DEVI uint32_t pack_bf2(float lo, float hi) { return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16); }
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+DEVI uint32_t pack_bf2(float lo, float hi) {
+  const v2bf v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
-// logistic for the activation epilogues; their results are rounded to bf16 or int8 right after
-DEVI float sigmoid_fast(float x) { return 1.f / (1.f + __expf(-x)); }
+// logistic for the activation epilogues (hardware exp and reciprocal); their results are rounded to bf16 or int8
+// right after, far coarser than these approximations
+DEVI float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 
 // ---- wave helpers ----------------------------------------------------------------------------------------------------
 
@@ -46,6 +46,11 @@ DEVI float wave_max_xor(float v, int width) {
 
 // wait for this wave's outstanding vector-memory operations (incl. global -> LDS transfers)
 DEVI void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// workgroup barrier for LDS pipelines: this wave's LDS operations complete, then s_barrier. Unlike __syncthreads()
+// it carries no memory fence, so the compiler does not drain the global -> LDS transfers still in flight for later
+// stages (the caller waits for the ones it needs with an explicit vmcnt first).
+DEVI void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---- C-ABI error reporting -------------------------------------------------------------------------------------------
 

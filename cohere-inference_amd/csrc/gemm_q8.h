@@ -1,0 +1,471 @@
+// W8A8 int8 GEMM kernel template for gfx950: dense (v_mfma_i32_16x16x64_i8) and 2:4 sparse
+// (v_smfmac_i32_16x16x128_i8), with the reference's fused epilogues. Instantiated by gemm_q8_dense.hip and
+// gemm_q8_sparse.hip; the C ABI entry points are in gemm_q8.hip.
+//
+// Semantics follow kernels/csrc/gemm_int8.cu (dense) and kernels/csrc/gemm_sparse.cu (sparse) of the reference:
+//   acc = sum_k X[m,k] W[n,k]                  int32, exact
+//   per-row scales:   x = fmul((float)acc, sx[m])
+//   grouped scales:   x = fmaf((float)acc_g, sx[m,g], x) over the K-groups g in order (gemm_int8.cu:146-163)
+//   v = bias ? fmaf(x, sw[n], bias[n]) : fmul(x, sw[n])
+//   epilogues BIAS / RESID / GLU / SILU_Q8 as gemm_int8.cu:201-288; I32 writes acc (parity hook).
+// The integer sums do not depend on the order of K, so any tile shape gives the same bits, and the sparse kernel
+// equals the dense one on the decompressed weights.
+//
+// gfx950 design:
+//  * The matrix cores compute the transposed tile D = W X^T: the MFMA/SMFMAC A operand is the weight (for the sparse
+//    kernel the instruction requires the sparse operand there), B the tokens. A lane then holds 4 consecutive output
+//    channels of one token: one token scale, a float4 of channel scales, and 8-byte (bf16) output stores.
+//  * K tiles of 128 bytes are copied global -> LDS by the load unit itself (global_load_lds_dwordx4: 1 KB per wave
+//    instruction, no staging registers) through a ST-stage ring: the next ST-1 tiles stream in while the matrix
+//    cores run on the current one. Each wave waits only for its own transfers of the tile it needs (vmcnt), then one
+//    plain s_barrier per tile (no memory fence, which would drain every transfer in flight).
+//  * LDS rows are 128 bytes (64 for compressed weights) with 16-byte chunks XOR-swizzled by row, so both the DMA
+//    writes (8 lanes per row) and the fragment reads (16 rows, one chunk) are bank-conflict free. The swizzle is
+//    applied on the global side: lane i of a DMA instruction lands in LDS slot i, so it fetches the chunk that
+//    belongs there.
+//  * Operand layouts (measured on gfx950): mfma_i32_16x16x64_i8 lane l holds row l%16, K bytes 16(l/16)..+15 of both
+//    A and B, and D rows 4(l/16)..+3 of column l%16. smfmac_i32_16x16x128_i8: A (compressed) lane l holds row l%16,
+//    the 16 kept bytes of K 32(l/16)..+31 with their selector word; B lane l holds column l%16, K 16(l/16)..+15 in
+//    bytes 0-15 and K 64+16(l/16)..+15 in bytes 16-31. kernels/sparse.py's compress_24 rows are therefore the A
+//    operand as stored, with no repacking.
+//  * The epilogue is a template parameter and runs from registers: the tile's token scales, channel scales and bias
+//    are copied to LDS when the kernel starts (no dependent global loads after the main loop), results are stored
+//    straight from the accumulators, and SILU_Q8 reduces each row's column group with lane shuffles and a small LDS
+//    table.
+//  * Workgroups are remapped so that consecutive tiles land on the same XCD (workgroups are dealt round-robin over
+//    the 8 XCDs, each with its own L2), then rastered in groups of 8 token tiles sharing a weight tile.
+#pragma once
+#include "common.h"
+
+namespace cohere_gemm {
+
+enum { EPI_BIAS = 0, EPI_RESID = 3, EPI_GLU = 4, EPI_SILU_Q8 = 5, EPI_I32 = 7 };
+
+struct GemmArgs {
+  const int8_t* X;       // tokens [M, K], row stride ldx
+  const float* sx;       // [M, ldsx] per-row (and K-group) scales
+  const int8_t* W;       // dense [N, K] or 2:4 kept values [N, K/2]
+  const int32_t* E;      // 2:4 selectors [N, K/32]
+  const float* sw;       // [N]
+  const uint16_t* bias;  // [N] bf16 or null
+  void* C;
+  const uint16_t* R;     // residual, bf16
+  float* qs;             // SILU_Q8 scales
+  int64_t ldx, ldsx, ldc, ldr, ldqs;
+  int M, N, K;
+  int group_steps;       // K steps per scale group (grouped only)
+  int qgroup;            // SILU_Q8 columns per scale
+  int epi;               // host-side dispatch only: the kernels take the epilogue as a template parameter
+  float alpha;
+};
+
+constexpr int LDS_BYTES = 160 * 1024;
+
+template <int BM, int BN, int WM, int WN, int ST, bool GROUPED, bool SPARSE>
+struct Tile {
+  static constexpr int NW = WM * WN, NT = NW * 64;
+  static constexpr int TM = BM / WM, TN = BN / WN, MI = TM / 16, NI = TN / 16;
+  static constexpr int X_STAGE = BM * 128;
+  static constexpr int W_STAGE = SPARSE ? BN * 64 : BN * 128;
+  static constexpr int E_STAGE = SPARSE ? BN * 16 : 0;
+  static constexpr int STAGE = X_STAGE + W_STAGE + E_STAGE;
+  static constexpr int PIPE = ST * STAGE;
+  static constexpr int PARAMS = (BM + 2 * BN) * 4;  // token scales, channel scales, bias (fp32)
+  static constexpr int GFIT = (LDS_BYTES - PIPE - PARAMS) / (BM * 4);
+  static constexpr int GMAX = GROUPED ? (GFIT < 32 ? GFIT : 32) : 0;  // K-groups whose token scales live in LDS
+  static constexpr int SMEM = PIPE + PARAMS + GMAX * BM * 4;
+  // 1 KB DMA instructions per stage: tokens (8 rows each), weights (8 dense rows / 16 compressed rows), selectors
+  // (one per wave, BN/NW rows)
+  static constexpr int X_SLOTS = BM / 8, W_SLOTS = SPARSE ? BN / 16 : BN / 8;
+  static constexpr int LPS = X_SLOTS / NW + W_SLOTS / NW + (SPARSE ? 1 : 0);  // per wave per stage
+  static_assert(TM % 16 == 0 && TN % 16 == 0, "tile shape");
+  static_assert(X_SLOTS % NW == 0 && W_SLOTS % NW == 0 && BN / NW <= 64, "DMA slots must split evenly over waves");
+  static_assert(LPS * (ST - 2 > 0 ? ST - 2 : 0) <= 63, "vmcnt range");
+  static_assert(SMEM <= LDS_BYTES, "LDS");
+  static_assert(BM * (BN / 16) * 4 <= PIPE, "SILU_Q8 row-max table reuses the pipeline buffers");
+  static_assert(!GROUPED || GMAX >= 1, "grouped tile needs room for scales");
+};
+
+DEVI void dma16(const void* g, char* lds_slot) {
+  __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds_slot, 16, 0, 0);
+}
+
+template <int N>
+DEVI void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// wait until at most `after` stages of this wave's DMA (LPS instructions each) are still in flight
+template <int LPS, int ST>
+DEVI void wait_stages(int after) {
+  if constexpr (ST >= 4) {
+    if (after >= 2) {
+      wait_vm<2 * LPS>();
+      return;
+    }
+  }
+  if constexpr (ST >= 3) {
+    if (after >= 1) {
+      wait_vm<LPS>();
+      return;
+    }
+  }
+  wait_vm<0>();
+}
+
+// 16-byte chunk `c` (0..7) of row `r` of a 128-byte-row tile
+DEVI int sw128(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// chunk `c` (0..3) of row `r` of a 64-byte-row tile
+DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
+
+template <int BM, int BN, int WM, int WN, int ST, int EPI, bool GROUPED, bool SPARSE>
+__global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) {
+  using T = Tile<BM, BN, WM, WN, ST, GROUPED, SPARSE>;
+  constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI, LPS = T::LPS;
+  __shared__ __attribute__((aligned(16))) char smem[T::SMEM];
+
+  const int M = p.M, N = p.N, K = p.K;
+  const int ntm = (M + BM - 1) / BM, ntn = N / BN, ntiles = ntm * ntn;
+  int t;
+  {  // XCD-aware remap: workgroup b runs on XCD b % 8; give each XCD a contiguous range of logical tiles
+    const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, per = ntiles >> 3, rem = ntiles & 7;
+    t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  }
+  constexpr int GM = 8;
+  const int gw = GM * ntn, first = (t / gw) * GM, gs = min(ntm - first, GM);
+  const int m0 = (first + (t % gw) % gs) * BM, n0 = ((t % gw) / gs) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int wm = wave / WN, wn = wave % WN;
+
+  const int KT = (K + 127) / 128;
+  const bool half_last = (K & 127) != 0;  // dense only: the last tile holds 64 K
+
+  // the epilogue's per-row / per-channel values, and (grouped) every group's token scales, copied to LDS before the
+  // first DMA; the first barrier of the main loop publishes them
+  float* pS = reinterpret_cast<float*>(smem + T::PIPE);
+  float* pW = pS + BM;
+  float* pB = pW + BN;
+  float* sS = pB + BN;
+  const int G = GROUPED ? K / (p.group_steps * (SPARSE ? 128 : 64)) : 1;
+  const bool scales_in_lds = GROUPED && G <= T::GMAX;
+  if constexpr (EPI != EPI_I32) {
+    for (int i = tid; i < BM + 2 * BN; i += NT) {
+      float v;
+      if (i < BM) v = GROUPED ? 1.f : p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
+      else if (i < BM + BN) v = p.sw[n0 + i - BM];
+      else v = p.bias ? bf2f(p.bias[n0 + i - BM - BN]) : 0.f;
+      pS[i] = v;
+    }
+  }
+  if (scales_in_lds) {
+    for (int i = tid; i < G * BM; i += NT) {
+      const int g = i / BM, r = i % BM;
+      sS[i] = p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+    }
+  }
+
+  auto issue = [&](int buf, int kt) {
+    char* base = smem + buf * T::STAGE;
+    const bool half = half_last && kt == KT - 1;
+    const int64_t k0 = (int64_t)kt * 128;
+#pragma unroll
+    for (int j = 0; j < T::X_SLOTS / NW; ++j) {  // tokens: 8 rows of 128 B per instruction
+      const int s = wave + j * NW;
+      const int r = s * 8 + (lane >> 3);
+      int lc = (lane & 7) ^ (r & 7);
+      if (half) lc &= 3;
+      dma16(p.X + (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + lc * 16, base + s * 1024);
+    }
+    char* wbase = base + T::X_STAGE;
+    if constexpr (!SPARSE) {
+#pragma unroll
+      for (int j = 0; j < T::W_SLOTS / NW; ++j) {
+        const int s = wave + j * NW;
+        const int r = s * 8 + (lane >> 3);
+        int lc = (lane & 7) ^ (r & 7);
+        if (half) lc &= 3;
+        dma16(p.W + (int64_t)(n0 + r) * K + k0 + lc * 16, wbase + s * 1024);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < T::W_SLOTS / NW; ++j) {  // kept values: 16 rows of 64 B per instruction
+        const int s = wave + j * NW;
+        const int r = s * 16 + (lane >> 2), lc = (lane & 3) ^ ((r >> 1) & 3);
+        dma16(p.W + (int64_t)(n0 + r) * (K / 2) + k0 / 2 + lc * 16, wbase + s * 1024);
+      }
+      // selectors: 16 B (4 words) a row; wave w brings rows [w BN/NW, (w+1) BN/NW)
+      constexpr int ER = BN / NW;
+      char* ebase = wbase + T::W_STAGE + wave * ER * 16;
+      const int r = wave * ER + lane;
+      if (lane < ER) dma16(p.E + (int64_t)(n0 + r) * (K / 32) + k0 / 32, ebase);
+    }
+  };
+
+  v4i acc[NI][MI];
+  v4f accf[GROUPED ? NI : 1][GROUPED ? MI : 1];
+#pragma unroll
+  for (int j = 0; j < NI; ++j)
+#pragma unroll
+    for (int i = 0; i < MI; ++i) acc[j][i] = v4i{0, 0, 0, 0};
+  if constexpr (GROUPED) {
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int i = 0; i < MI; ++i) accf[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // fold the finished K-group's int32 sums into fp32 with each token's scale of that group
+  auto fold = [&](int g) {
+    if constexpr (GROUPED) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * TM + i * 16 + (lane & 15);
+        const float s = scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], s, accf[j][i][q]);
+          acc[j][i] = v4i{0, 0, 0, 0};
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int s = 0; s < ST - 1; ++s)
+    if (s < KT) issue(s, s);
+  int kstep = 0;
+  for (int kt = 0; kt < KT; ++kt) {
+    wait_stages<LPS, ST>(min(KT - 1 - kt, ST - 2));
+    lds_barrier();
+    if (kt + ST - 1 < KT) issue((kt + ST - 1) % ST, kt + ST - 1);
+    const char* xs = smem + (kt % ST) * T::STAGE;
+    const char* ws = xs + T::X_STAGE;
+    if constexpr (!SPARSE) {
+      const bool two = !(half_last && kt == KT - 1);
+      v4i bx[2][MI], aw[2][NI];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 1 && !two) break;
+        const int lc = s * 4 + (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          bx[s][i] = *reinterpret_cast<const v4i*>(xs + sw128(wm * TM + i * 16 + (lane & 15), lc));
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+          aw[s][j] = *reinterpret_cast<const v4i*>(ws + sw128(wn * TN + j * 16 + (lane & 15), lc));
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 1 && !two) break;
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int i = 0; i < MI; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw[s][j], bx[s][i], acc[j][i], 0, 0, 0);
+        if constexpr (GROUPED) {
+          ++kstep;
+          if (kstep % p.group_steps == 0) fold(kstep / p.group_steps - 1);
+        }
+      }
+    } else {
+      const char* es = ws + T::W_STAGE;
+      v8i bx[MI];
+      v4i aw[NI];
+      int ix[NI];
+      const int h = lane >> 4;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int r = wm * TM + i * 16 + (lane & 15);
+        const v4i lo = *reinterpret_cast<const v4i*>(xs + sw128(r, h));
+        const v4i hi = *reinterpret_cast<const v4i*>(xs + sw128(r, 4 + h));
+        bx[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int r = wn * TN + j * 16 + (lane & 15);
+        aw[j] = *reinterpret_cast<const v4i*>(ws + sw64(r, h));
+        ix[j] = *reinterpret_cast<const int*>(es + r * 16 + h * 4);
+      }
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+          acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(aw[j], bx[i], acc[j][i], ix[j], 0, 0);
+      if constexpr (GROUPED) {
+        ++kstep;
+        if (kstep % p.group_steps == 0) fold(kstep / p.group_steps - 1);
+      }
+    }
+  }
+
+  // ---- epilogue, from registers --------------------------------------------------------------------------------
+  const int ml0 = wm * TM + (lane & 15);      // + i * 16
+  const int nl0 = wn * TN + (lane >> 4) * 4;  // + j * 16
+  if constexpr (EPI == EPI_I32) {
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const int m = m0 + ml0 + i * 16;
+      if (m >= M) continue;
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+        *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(p.C) + (int64_t)m * p.ldc + n0 + nl0 + j * 16) = acc[j][i];
+    }
+    return;
+  } else {
+    // v = dequantized value (+ bias), in place of the accumulators
+    v4f val[NI][MI];
+    {
+      float srow[MI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) srow[i] = pS[ml0 + i * 16];
+      const bool has_bias = p.bias != nullptr;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const v4f w4 = *reinterpret_cast<const v4f*>(pW + nl0 + j * 16);
+        const v4f b4 = *reinterpret_cast<const v4f*>(pB + nl0 + j * 16);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float x = GROUPED ? accf[j][i][r] : (float)acc[j][i][r] * srow[i];
+            val[j][i][r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
+          }
+      }
+    }
+    if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID) {
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = m0 + ml0 + i * 16;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int n = n0 + nl0 + j * 16;
+          uint2 o;
+          if constexpr (EPI == EPI_RESID) {
+            const uint2 rv = *reinterpret_cast<const uint2*>(p.R + (int64_t)m * p.ldr + n);
+            const float y0 = round_bf(val[j][i][0]), y1 = round_bf(val[j][i][1]);
+            const float y2 = round_bf(val[j][i][2]), y3 = round_bf(val[j][i][3]);
+            o.x = pack_bf2(__builtin_fmaf(p.alpha, y0, __uint_as_float(rv.x << 16)),
+                           __builtin_fmaf(p.alpha, y1, __uint_as_float(rv.x & 0xffff0000u)));
+            o.y = pack_bf2(__builtin_fmaf(p.alpha, y2, __uint_as_float(rv.y << 16)),
+                           __builtin_fmaf(p.alpha, y3, __uint_as_float(rv.y & 0xffff0000u)));
+          } else {
+            o.x = pack_bf2(val[j][i][0], val[j][i][1]);
+            o.y = pack_bf2(val[j][i][2], val[j][i][3]);
+          }
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n) = o;
+        }
+      }
+    } else if constexpr (EPI == EPI_GLU) {
+      // interleaved (a, gate) channel pairs are adjacent in a lane: output column n / 2
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int m = m0 + ml0 + i * 16;
+        if (m >= M) continue;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int n = n0 + nl0 + j * 16;
+          const uint32_t o = pack_bf2(round_bf(val[j][i][0]) * sigmoid_fast(round_bf(val[j][i][1])),
+                                      round_bf(val[j][i][2]) * sigmoid_fast(round_bf(val[j][i][3])));
+          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n / 2) = o;
+        }
+      }
+    } else if constexpr (EPI == EPI_SILU_Q8) {
+      // u = bf16(silu(bf16(v))); the max |u| of each (row, 16-column block) across the 4 lanes holding it, into an
+      // LDS table [BM][BN/16] (over the pipeline buffers, free now); then each lane reads its group's blocks
+      constexpr int CB = BN / 16;
+      float* red = reinterpret_cast<float*>(smem);
+      lds_barrier();  // every wave is done reading the pipeline buffers
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          float mx = 0.f;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float tv = round_bf(val[j][i][r]);
+            val[j][i][r] = round_bf(tv * sigmoid_fast(tv));
+            mx = fmaxf(mx, fabsf(val[j][i][r]));
+          }
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          if ((lane >> 4) == 0) red[(ml0 + i * 16) * CB + (wn * TN + j * 16) / 16] = mx;
+        }
+      __syncthreads();
+      const int blocks = p.qgroup / 16;
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        const int rl = ml0 + i * 16, m = m0 + rl;
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+          const int cb = (wn * TN + j * 16) / 16, g0 = cb - cb % blocks;
+          float mx = 0.f;
+          for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, red[rl * CB + g0 + b]);
+          const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+          uint32_t q = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int qi = (int)rintf(fminf(fmaxf(val[j][i][r] * inv, -127.f), 127.f));
+            q |= (uint32_t)(qi & 0xff) << (8 * r);
+          }
+          if (m < M) {
+            const int n = n0 + nl0 + j * 16;
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n) = q;
+            if ((lane >> 4) == 0 && cb == g0) p.qs[(int64_t)m * p.ldqs + (n0 + cb * 16) / p.qgroup] = sc;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, int WM, int WN, int ST, int EPI, bool GROUPED, bool SPARSE>
+void launch_tile(const GemmArgs& p, hipStream_t s) {
+  const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
+  gemm_q8_kernel<BM, BN, WM, WN, ST, EPI, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
+}
+
+// tile ids (tokens x channels, waves M x N, pipeline stages):
+//   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
+//   5 32x128 (1x4, 4)    6 256x256 (2x4, 2 dense / 3 sparse)        7 64x64 (2x2, 4)    8 256x128 (4x2, 3)
+//   9 128x256 (2x4, 3)
+struct TileInfo {
+  int bm, bn;
+  bool grouped_ok;
+};
+constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
+                              {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
+                              {256, 128, true}, {128, 256, true}};
+constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
+
+// launches tile `tile` for one (SPARSE, EPI, GROUPED); false when the tile has no such instantiation
+template <bool SPARSE, int EPI, bool GROUPED>
+bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
+  switch (tile) {
+    case 0: launch_tile<128, 128, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 3: launch_tile<64, 128, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 4: launch_tile<64, 256, 1, 4, 3, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 5: launch_tile<32, 128, 1, 4, 4, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 7: launch_tile<64, 64, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 8: launch_tile<256, 128, 4, 2, 3, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 9: launch_tile<128, 256, 2, 4, 3, EPI, GROUPED, SPARSE>(p, s); return true;
+    default: break;
+  }
+  if constexpr (!GROUPED) {
+    switch (tile) {
+      case 1: launch_tile<128, 256, 2, 2, 3, EPI, false, SPARSE>(p, s); return true;
+      case 2: launch_tile<256, 128, 2, 2, 3, EPI, false, SPARSE>(p, s); return true;
+      case 6: launch_tile<256, 256, 2, 4, SPARSE ? 3 : 2, EPI, false, SPARSE>(p, s); return true;
+      default: break;
+    }
+  }
+  return false;
+}
+
+// instantiated in gemm_q8_dense.hip / gemm_q8_sparse.hip
+template <bool SPARSE>
+bool launch_gemm(int tile, int epi, bool grouped, const GemmArgs& p, hipStream_t s);
+
+}  // namespace cohere_gemm
