@@ -1,4 +1,16 @@
 // C ABI of the W8A8 int8 GEMMs (include/cohere_hip.h): argument checks, the reference's config-id semantics, the
+// choice of gfx950 tile, and dispatch to the kernel instantiations (gemm_q8.h, gemm_q8_dense.hip, gemm_q8_sparse.hip).
+#include "cohere_hip.h"
+#include "gemm_q8.h"
+
+#include <string>
+
+namespace {
+
+using namespace cohere_gemm;
+
+int g_tile_override = -1;
+
 // gfx950 tile choice: the largest tile that still gives (nearly) every CU a workgroup; with fewer tiles than CUs,
 // the shape with the most workgroups. SILU_Q8 needs whole scale groups inside a tile.
 int num_cus() {
