@@ -46,7 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder"], default=None,
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy"], default=None,
                     help="run one part only (for rocprofv3 runs)")
     ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
     return ap.parse_args()
@@ -106,6 +106,18 @@ def time_graph(g, replays):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / replays
+
+
+def committed_traffic(which: str):
+    path = os.path.join(ROOT, "profiles", "gemm_sp_config1_traffic.json")
+    try:
+        table = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    from kernels.cuda_ext import ext  # noqa: F401
+    key = table.get("up" if "up" in which else "down")
+    return None if key is None else {"bytes": key["bytes"], "kernel": key["kernel"],
+                                     "source": "profiles/gemm_sp_config1.md"}
 
 
 def cpu_baseline(target_s=10.0):
@@ -284,6 +296,21 @@ def main():
                               "ops_per_launch": dom[2], "ms_per_launch": round(dom[1], 5),
                               "note": "int8 TOPS, dense-equivalent (2*M*N*K) against the 2:4 SMFMAC peak"}
         result["kernels_ms"] = {"sparse_up": round(ms_up, 5), "sparse_down": round(ms_dn, 5)}
+        # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary of this command
+        # (FETCH_SIZE + TCC_EA0 write requests, calibrated on a plain copy); null when the profiled kernel differs
+        result["roofline"]["traffic"] = committed_traffic(dom[0])
+
+    if args.only == "copy":
+        # calibration for the HBM byte counters: a plain device copy of a known size, 1 GiB read + 1 GiB written,
+        # its source evicted from the caches first by writing another 512 MiB
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        evict = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+        for _ in range(2):
+            evict.fill_(2)
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["copy_bytes"] = src.numel()
 
     if not args.no_extras and args.only in (None, "dense"):
         def dense():
