@@ -35,6 +35,8 @@
 //  * Workgroups are remapped so that consecutive tiles land on the same XCD (workgroups are dealt round-robin over
 //    the 8 XCDs, each with its own L2), then rastered in groups of 8 token tiles sharing a weight tile.
 #pragma once
+#include <type_traits>
+
 #include "common.h"
 
 namespace cohere_gemm {
@@ -53,7 +55,7 @@ struct GemmArgs {
   float* qs;             // SILU_Q8 scales
   int64_t ldx, ldsx, ldc, ldr, ldqs;
   int M, N, K;
-  int group_steps;       // K steps per scale group (grouped only)
+  int group;             // K per token-scale group (group == K: one scale per row)
   int qgroup;            // SILU_Q8 columns per scale
   int epi;               // host-side dispatch only: the kernels take the epilogue as a template parameter
   float alpha;
@@ -61,10 +63,15 @@ struct GemmArgs {
 
 constexpr int LDS_BYTES = 160 * 1024;
 
-template <int BM, int BN, int WM, int WN, int ST, bool GROUPED, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, int MS, bool GROUPED, bool SPARSE>
 struct Tile {
   static constexpr int NW = WM * WN, NT = NW * 64;
-  static constexpr int TM = BM / WM, TN = BN / WN, MI = TM / 16, NI = TN / 16;
+  static constexpr int TM = BM / WM, TN = BN / WN, MI = TM / MS, NI = TN / MS;
+  // K per matrix instruction, instructions per 128-byte K tile, values per lane per instruction
+  static constexpr int KSTEP = MS == 16 ? (SPARSE ? 128 : 64) : (SPARSE ? 64 : 32);
+  static constexpr int SPS = 128 / KSTEP;
+  static constexpr int RPL = MS == 16 ? 4 : 16;
+  static constexpr bool PF = NW <= 4;  // one wave per SIMD: double-buffer the fragments within the wave
   static constexpr int X_STAGE = BM * 128;
   static constexpr int W_STAGE = SPARSE ? BN * 64 : BN * 128;
   static constexpr int E_STAGE = SPARSE ? BN * 16 : 0;
@@ -78,11 +85,12 @@ struct Tile {
   // (one per wave, BN/NW rows)
   static constexpr int X_SLOTS = BM / 8, W_SLOTS = SPARSE ? BN / 16 : BN / 8;
   static constexpr int LPS = X_SLOTS / NW + W_SLOTS / NW + (SPARSE ? 1 : 0);  // per wave per stage
-  static_assert(TM % 16 == 0 && TN % 16 == 0, "tile shape");
+  static_assert(MS == 16 || MS == 32, "matrix instruction size");
+  static_assert(TM % MS == 0 && TN % MS == 0 && MI >= 1 && NI >= 1, "tile shape");
   static_assert(X_SLOTS % NW == 0 && W_SLOTS % NW == 0 && BN / NW <= 64, "DMA slots must split evenly over waves");
-  static_assert(LPS * (ST - 2 > 0 ? ST - 2 : 0) <= 63, "vmcnt range");
+  static_assert(LPS * (ST - 1) <= 63 && ST >= 2 && ST <= 4, "vmcnt range");
   static_assert(SMEM <= LDS_BYTES, "LDS");
-  static_assert(BM * (BN / 16) * 4 <= PIPE, "SILU_Q8 row-max table reuses the pipeline buffers");
+  static_assert(BM * (BN / MS) * 4 <= PIPE, "SILU_Q8 row-max table reuses the pipeline buffers");
   static_assert(!GROUPED || GMAX >= 1, "grouped tile needs room for scales");
 };
 
@@ -99,12 +107,18 @@ DEVI void wait_vm() {
 template <int LPS, int ST>
 DEVI void wait_stages(int after) {
   if constexpr (ST >= 4) {
+    if (after >= 3) {
+      wait_vm<3 * LPS>();
+      return;
+    }
+  }
+  if constexpr (ST >= 3) {
     if (after >= 2) {
       wait_vm<2 * LPS>();
       return;
     }
   }
-  if constexpr (ST >= 3) {
+  if constexpr (ST >= 2) {
     if (after >= 1) {
       wait_vm<LPS>();
       return;
@@ -118,10 +132,13 @@ DEVI int sw128(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 // chunk `c` (0..3) of row `r` of a 64-byte-row tile
 DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
-template <int BM, int BN, int WM, int WN, int ST, int EPI, bool GROUPED, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE>
 __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) {
-  using T = Tile<BM, BN, WM, WN, ST, GROUPED, SPARSE>;
+  using T = Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>;
   constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI, LPS = T::LPS;
+  constexpr int KSTEP = T::KSTEP, SPS = T::SPS, RPL = T::RPL;
+  using Acc = typename std::conditional<MS == 16, v4i, v16i>::type;
+  using AccF = typename std::conditional<MS == 16, v4f, v16f>::type;
   __shared__ __attribute__((aligned(16))) char smem[T::SMEM];
 
   const int M = p.M, N = p.N, K = p.K;
@@ -140,14 +157,16 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 
   const int KT = (K + 127) / 128;
   const bool half_last = (K & 127) != 0;  // dense only: the last tile holds 64 K
+  const int NSTEPS = K / KSTEP;
 
   // the epilogue's per-row / per-channel values, and (grouped) every group's token scales, copied to LDS before the
-  // first DMA; the first barrier of the main loop publishes them
+  // first DMA; the first barrier publishes them
   float* pS = reinterpret_cast<float*>(smem + T::PIPE);
   float* pW = pS + BM;
   float* pB = pW + BN;
   float* sS = pB + BN;
-  const int G = GROUPED ? K / (p.group_steps * (SPARSE ? 128 : 64)) : 1;
+  const int group_steps = GROUPED ? p.group / KSTEP : 1;
+  const int G = GROUPED ? K / p.group : 1;
   const bool scales_in_lds = GROUPED && G <= T::GMAX;
   if constexpr (EPI != EPI_I32) {
     for (int i = tid; i < BM + 2 * BN; i += NT) {
@@ -202,180 +221,208 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     }
   };
 
-  v4i acc[NI][MI];
-  v4f accf[GROUPED ? NI : 1][GROUPED ? MI : 1];
+  Acc acc[NI][MI];
+  AccF accf[GROUPED ? NI : 1][GROUPED ? MI : 1];
 #pragma unroll
   for (int j = 0; j < NI; ++j)
 #pragma unroll
-    for (int i = 0; i < MI; ++i) acc[j][i] = v4i{0, 0, 0, 0};
-  if constexpr (GROUPED) {
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-#pragma unroll
-      for (int i = 0; i < MI; ++i) accf[j][i] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int i = 0; i < MI; ++i) {
+      acc[j][i] = Acc{};
+      if constexpr (GROUPED) accf[j][i] = AccF{};
+    }
+
+  // a lane's token row within the tile for instruction-block row i, and its first channel for block column j and
+  // group q of 4 consecutive channels (16x16: one group of 4; 32x32: four groups, 8 channels apart)
+  const int lrow = MS == 16 ? (lane & 15) : (lane & 31);
+  const int lhi = MS == 16 ? (lane >> 4) : (lane >> 5);
+  auto tok = [&](int i) { return wm * TM + i * MS + lrow; };
+  auto chan = [&](int j, int q) { return wn * TN + j * MS + (MS == 16 ? lhi * 4 : 8 * q + 4 * lhi); };
 
   // fold the finished K-group's int32 sums into fp32 with each token's scale of that group
   auto fold = [&](int g) {
     if constexpr (GROUPED) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int r = wm * TM + i * 16 + (lane & 15);
-        const float s = scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+        const int r = tok(i);
+        const float sc = scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], s, accf[j][i][q]);
-          acc[j][i] = v4i{0, 0, 0, 0};
+          for (int q = 0; q < RPL; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], sc, accf[j][i][q]);
+          acc[j][i] = Acc{};
         }
       }
     }
   };
 
-#pragma unroll
-  for (int s = 0; s < ST - 1; ++s)
-    if (s < KT) issue(s, s);
-  int kstep = 0;
-  for (int kt = 0; kt < KT; ++kt) {
-    wait_stages<LPS, ST>(min(KT - 1 - kt, ST - 2));
-    lds_barrier();
-    if (kt + ST - 1 < KT) issue((kt + ST - 1) % ST, kt + ST - 1);
-    const char* xs = smem + (kt % ST) * T::STAGE;
+  // ---- main loop: ST-stage DMA ring; matrix-core fragments of K step u read from stage u / SPS ------------------
+  struct Frags {
+    typename std::conditional<SPARSE, v8i, v4i>::type bx[MI];
+    v4i aw[NI];
+    int ix[SPARSE ? NI : 1];
+  };
+  auto load_frags = [&](Frags& F, int u) {
+    const int st = u / SPS, s = u % SPS;
+    const char* xs = smem + (st % ST) * T::STAGE;
     const char* ws = xs + T::X_STAGE;
     if constexpr (!SPARSE) {
-      const bool two = !(half_last && kt == KT - 1);
-      v4i bx[2][MI], aw[2][NI];
+      // 16x16x64: chunk 4s + lane/16 of rows lane%16; 32x32x32: chunk 2s + lane/32 of rows lane%32
+      const int lc = MS == 16 ? s * 4 + lhi : s * 2 + lhi;
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 1 && !two) break;
-        const int lc = s * 4 + (lane >> 4);
+      for (int i = 0; i < MI; ++i) F.bx[i] = *reinterpret_cast<const v4i*>(xs + sw128(wm * TM + i * MS + lrow, lc));
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
-          bx[s][i] = *reinterpret_cast<const v4i*>(xs + sw128(wm * TM + i * 16 + (lane & 15), lc));
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-          aw[s][j] = *reinterpret_cast<const v4i*>(ws + sw128(wn * TN + j * 16 + (lane & 15), lc));
-      }
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 1 && !two) break;
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-#pragma unroll
-          for (int i = 0; i < MI; ++i)
-            acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aw[s][j], bx[s][i], acc[j][i], 0, 0, 0);
-        if constexpr (GROUPED) {
-          ++kstep;
-          if (kstep % p.group_steps == 0) fold(kstep / p.group_steps - 1);
-        }
-      }
+      for (int j = 0; j < NI; ++j) F.aw[j] = *reinterpret_cast<const v4i*>(ws + sw128(wn * TN + j * MS + lrow, lc));
     } else {
       const char* es = ws + T::W_STAGE;
-      v8i bx[MI];
-      v4i aw[NI];
-      int ix[NI];
-      const int h = lane >> 4;
+      // B (tokens): 16x16x128 reads chunks h and 4 + h (h = lane/16); 32x32x64 step s reads 4s + h and 4s + 2 + h
+      // (h = lane/32). A (kept weights): compressed chunk h / 2s + h, and the selector word of the same 32 K.
+      const int c0 = MS == 16 ? lhi : 4 * s + lhi, c1 = MS == 16 ? 4 + lhi : 4 * s + 2 + lhi;
+      const int ca = MS == 16 ? lhi : 2 * s + lhi;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int r = wm * TM + i * 16 + (lane & 15);
-        const v4i lo = *reinterpret_cast<const v4i*>(xs + sw128(r, h));
-        const v4i hi = *reinterpret_cast<const v4i*>(xs + sw128(r, 4 + h));
-        bx[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        const int r = wm * TM + i * MS + lrow;
+        const v4i lo = *reinterpret_cast<const v4i*>(xs + sw128(r, c0));
+        const v4i hi = *reinterpret_cast<const v4i*>(xs + sw128(r, c1));
+        F.bx[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
 #pragma unroll
       for (int j = 0; j < NI; ++j) {
-        const int r = wn * TN + j * 16 + (lane & 15);
-        aw[j] = *reinterpret_cast<const v4i*>(ws + sw64(r, h));
-        ix[j] = *reinterpret_cast<const int*>(es + r * 16 + h * 4);
+        const int r = wn * TN + j * MS + lrow;
+        F.aw[j] = *reinterpret_cast<const v4i*>(ws + sw64(r, ca));
+        F.ix[j] = *reinterpret_cast<const int*>(es + r * 16 + ca * 4);
       }
+    }
+  };
+  int kstep = 0;
+  auto mma = [&](const Frags& F) {
 #pragma unroll
-      for (int j = 0; j < NI; ++j)
+    for (int j = 0; j < NI; ++j)
 #pragma unroll
-        for (int i = 0; i < MI; ++i)
-          acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(aw[j], bx[i], acc[j][i], ix[j], 0, 0);
-      if constexpr (GROUPED) {
-        ++kstep;
-        if (kstep % p.group_steps == 0) fold(kstep / p.group_steps - 1);
+      for (int i = 0; i < MI; ++i) {
+        if constexpr (SPARSE && MS == 16)
+          acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+        else if constexpr (SPARSE)
+          acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+        else if constexpr (MS == 16)
+          acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
+        else
+          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
       }
+    if constexpr (GROUPED) {
+      ++kstep;
+      if (kstep % group_steps == 0) fold(kstep / group_steps - 1);
+    }
+  };
+  // before reading step u, the first of stage t = u / SPS: stage t landed everywhere and stage t - 1 is free, so
+  // stage t - 1 + ST can stream into its buffer
+  auto enter_stage = [&](int t) {
+    wait_stages<LPS, ST>(min(KT - 1 - t, ST - 2));
+    lds_barrier();
+    if (t - 1 + ST < KT) issue((t - 1 + ST) % ST, t - 1 + ST);
+  };
+
+#pragma unroll
+  for (int s = 0; s < ST; ++s)
+    if (s < KT) issue(s, s);
+  wait_stages<LPS, ST>(min(KT - 1, ST - 1));
+  lds_barrier();
+  if constexpr (T::PF) {
+    // fragments of step u + 1 are read while the matrix cores work on step u
+    Frags F0, F1;
+    load_frags(F0, 0);
+    for (int u = 0; u < NSTEPS; u += 2) {
+      if (u + 1 < NSTEPS) {
+        if ((u + 1) % SPS == 0) enter_stage((u + 1) / SPS);
+        load_frags(F1, u + 1);
+      }
+      mma(F0);
+      if (u + 1 < NSTEPS) {
+        if (u + 2 < NSTEPS) {
+          if ((u + 2) % SPS == 0) enter_stage((u + 2) / SPS);
+          load_frags(F0, u + 2);
+        }
+        mma(F1);
+      }
+    }
+  } else {
+    // two waves per SIMD hide each other's LDS latency
+    Frags F0;
+    for (int u = 0; u < NSTEPS; ++u) {
+      if (u > 0 && u % SPS == 0) enter_stage(u / SPS);
+      load_frags(F0, u);
+      mma(F0);
     }
   }
 
   // ---- epilogue, from registers --------------------------------------------------------------------------------
-  const int ml0 = wm * TM + (lane & 15);      // + i * 16
-  const int nl0 = wn * TN + (lane >> 4) * 4;  // + j * 16
+  constexpr int NQ = RPL / 4;  // groups of 4 consecutive channels per lane per block
   if constexpr (EPI == EPI_I32) {
 #pragma unroll
     for (int i = 0; i < MI; ++i) {
-      const int m = m0 + ml0 + i * 16;
+      const int m = m0 + tok(i);
       if (m >= M) continue;
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(p.C) + (int64_t)m * p.ldc + n0 + nl0 + j * 16) = acc[j][i];
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+          *reinterpret_cast<v4i*>(reinterpret_cast<int32_t*>(p.C) + (int64_t)m * p.ldc + n0 + chan(j, q)) =
+              v4i{acc[j][i][4 * q], acc[j][i][4 * q + 1], acc[j][i][4 * q + 2], acc[j][i][4 * q + 3]};
     }
     return;
   } else {
-    // v = dequantized value (+ bias), in place of the accumulators
-    v4f val[NI][MI];
-    {
-      float srow[MI];
+    // dequantized value (+ bias) of block (j, i), values 4q..4q+3: computed where it is stored, so no second copy
+    // of the accumulators is held
+    float srow[MI];
 #pragma unroll
-      for (int i = 0; i < MI; ++i) srow[i] = pS[ml0 + i * 16];
-      const bool has_bias = p.bias != nullptr;
+    for (int i = 0; i < MI; ++i) srow[i] = pS[tok(i)];
+    const bool has_bias = p.bias != nullptr;
+    auto dequant = [&](int j, int i, int q, float (&v)[4]) {
+      const v4f w4 = *reinterpret_cast<const v4f*>(pW + chan(j, q));
+      const v4f b4 = *reinterpret_cast<const v4f*>(pB + chan(j, q));
 #pragma unroll
-      for (int j = 0; j < NI; ++j) {
-        const v4f w4 = *reinterpret_cast<const v4f*>(pW + nl0 + j * 16);
-        const v4f b4 = *reinterpret_cast<const v4f*>(pB + nl0 + j * 16);
-#pragma unroll
-        for (int i = 0; i < MI; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float x = GROUPED ? accf[j][i][r] : (float)acc[j][i][r] * srow[i];
-            val[j][i][r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
-          }
+      for (int r = 0; r < 4; ++r) {
+        const float x = GROUPED ? accf[j][i][4 * q + r] : (float)acc[j][i][4 * q + r] * srow[i];
+        v[r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
       }
-    }
-    if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID) {
+    };
+    if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID || EPI == EPI_GLU) {
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int m = m0 + ml0 + i * 16;
+        const int m = m0 + tok(i);
         if (m >= M) continue;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int n = n0 + nl0 + j * 16;
-          uint2 o;
-          if constexpr (EPI == EPI_RESID) {
-            const uint2 rv = *reinterpret_cast<const uint2*>(p.R + (int64_t)m * p.ldr + n);
-            const float y0 = round_bf(val[j][i][0]), y1 = round_bf(val[j][i][1]);
-            const float y2 = round_bf(val[j][i][2]), y3 = round_bf(val[j][i][3]);
-            o.x = pack_bf2(__builtin_fmaf(p.alpha, y0, __uint_as_float(rv.x << 16)),
-                           __builtin_fmaf(p.alpha, y1, __uint_as_float(rv.x & 0xffff0000u)));
-            o.y = pack_bf2(__builtin_fmaf(p.alpha, y2, __uint_as_float(rv.y << 16)),
-                           __builtin_fmaf(p.alpha, y3, __uint_as_float(rv.y & 0xffff0000u)));
-          } else {
-            o.x = pack_bf2(val[j][i][0], val[j][i][1]);
-            o.y = pack_bf2(val[j][i][2], val[j][i][3]);
+        for (int j = 0; j < NI; ++j)
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            const int n = n0 + chan(j, q);
+            float v[4];
+            dequant(j, i, q, v);
+            if constexpr (EPI == EPI_GLU) {
+              // interleaved (a, gate) channel pairs are adjacent in a lane: output column n / 2
+              const uint32_t o = pack_bf2(round_bf(v[0]) * sigmoid_fast(round_bf(v[1])),
+                                          round_bf(v[2]) * sigmoid_fast(round_bf(v[3])));
+              *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n / 2) = o;
+            } else {
+              uint2 o;
+              if constexpr (EPI == EPI_RESID) {
+                const uint2 rv = *reinterpret_cast<const uint2*>(p.R + (int64_t)m * p.ldr + n);
+                o.x = pack_bf2(__builtin_fmaf(p.alpha, round_bf(v[0]), __uint_as_float(rv.x << 16)),
+                               __builtin_fmaf(p.alpha, round_bf(v[1]), __uint_as_float(rv.x & 0xffff0000u)));
+                o.y = pack_bf2(__builtin_fmaf(p.alpha, round_bf(v[2]), __uint_as_float(rv.y << 16)),
+                               __builtin_fmaf(p.alpha, round_bf(v[3]), __uint_as_float(rv.y & 0xffff0000u)));
+              } else {
+                o.x = pack_bf2(v[0], v[1]);
+                o.y = pack_bf2(v[2], v[3]);
+              }
+              *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n) = o;
+            }
           }
-          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n) = o;
-        }
-      }
-    } else if constexpr (EPI == EPI_GLU) {
-      // interleaved (a, gate) channel pairs are adjacent in a lane: output column n / 2
-#pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int m = m0 + ml0 + i * 16;
-        if (m >= M) continue;
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-          const int n = n0 + nl0 + j * 16;
-          const uint32_t o = pack_bf2(round_bf(val[j][i][0]) * sigmoid_fast(round_bf(val[j][i][1])),
-                                      round_bf(val[j][i][2]) * sigmoid_fast(round_bf(val[j][i][3])));
-          *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n / 2) = o;
-        }
       }
     } else if constexpr (EPI == EPI_SILU_Q8) {
-      // u = bf16(silu(bf16(v))); the max |u| of each (row, 16-column block) across the 4 lanes holding it, into an
-      // LDS table [BM][BN/16] (over the pipeline buffers, free now); then each lane reads its group's blocks
-      constexpr int CB = BN / 16;
+      // u = bf16(silu(bf16(v))), kept (as float bits) in the accumulator registers; the max |u| of each (row,
+      // MS-column block) across the lanes holding it goes to an LDS table [BM][BN/MS] (over the pipeline buffers,
+      // free now); then each lane reads its group's blocks and quantizes
+      constexpr int CB = BN / MS;
       float* red = reinterpret_cast<float*>(smem);
       lds_barrier();  // every wave is done reading the pipeline buffers
 #pragma unroll
@@ -384,80 +431,98 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
         for (int i = 0; i < MI; ++i) {
           float mx = 0.f;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float tv = round_bf(val[j][i][r]);
-            val[j][i][r] = round_bf(tv * sigmoid_fast(tv));
-            mx = fmaxf(mx, fabsf(val[j][i][r]));
+          for (int q = 0; q < NQ; ++q) {
+            float v[4];
+            dequant(j, i, q, v);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float tv = round_bf(v[r]);
+              const float u = round_bf(tv * sigmoid_fast(tv));
+              mx = fmaxf(mx, fabsf(u));
+              acc[j][i][4 * q + r] = __float_as_int(u);
+            }
           }
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          if ((lane >> 4) == 0) red[(ml0 + i * 16) * CB + (wn * TN + j * 16) / 16] = mx;
+          if constexpr (MS == 16) {
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          } else {
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          }
+          if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
         }
       __syncthreads();
-      const int blocks = p.qgroup / 16;
+      const int blocks = p.qgroup / MS;
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int rl = ml0 + i * 16, m = m0 + rl;
+        const int rl = tok(i), m = m0 + rl;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
-          const int cb = (wn * TN + j * 16) / 16, g0 = cb - cb % blocks;
+          const int cb = (wn * TN + j * MS) / MS, g0 = cb - cb % blocks;
           float mx = 0.f;
           for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, red[rl * CB + g0 + b]);
           const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
-          uint32_t q = 0;
+          if (m >= M) continue;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int qi = (int)rintf(fminf(fmaxf(val[j][i][r] * inv, -127.f), 127.f));
-            q |= (uint32_t)(qi & 0xff) << (8 * r);
+          for (int q = 0; q < NQ; ++q) {
+            uint32_t o = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float u = __int_as_float(acc[j][i][4 * q + r]);
+              const int qi = (int)rintf(fminf(fmaxf(u * inv, -127.f), 127.f));
+              o |= (uint32_t)(qi & 0xff) << (8 * r);
+            }
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n0 + chan(j, q)) = o;
           }
-          if (m < M) {
-            const int n = n0 + nl0 + j * 16;
-            *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n) = q;
-            if ((lane >> 4) == 0 && cb == g0) p.qs[(int64_t)m * p.ldqs + (n0 + cb * 16) / p.qgroup] = sc;
-          }
+          if (lhi == 0 && cb == g0) p.qs[(int64_t)m * p.ldqs + (n0 + cb * MS) / p.qgroup] = sc;
         }
       }
     }
   }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int EPI, bool GROUPED, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE>
 void launch_tile(const GemmArgs& p, hipStream_t s) {
   const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
-  gemm_q8_kernel<BM, BN, WM, WN, ST, EPI, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
+  gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
 }
 
 // tile ids (tokens x channels, waves M x N, pipeline stages):
 //   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
 //   5 32x128 (1x4, 4)    6 256x256 (2x4, 2 dense / 3 sparse)        7 64x64 (2x2, 4)    8 256x128 (4x2, 3)
-//   9 128x256 (2x4, 3)
+//   9 128x256 (2x4, 3)   10 256x256 (4x2, 2 dense / 3 sparse)   11 256x128 (2x2, 3)   12 128x128 (2x2, 4)
+//   13 128x256 (2x2, 3); tiles 11-13 use the 32x32 matrix instructions, the others 16x16
 struct TileInfo {
   int bm, bn;
   bool grouped_ok;
 };
 constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
                               {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
-                              {256, 128, true}, {128, 256, true}};
+                              {256, 128, true}, {128, 256, true},  {256, 256, false}, {256, 128, false},
+                              {128, 128, true}, {128, 256, false}};
 constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
 
 // launches tile `tile` for one (SPARSE, EPI, GROUPED); false when the tile has no such instantiation
 template <bool SPARSE, int EPI, bool GROUPED>
 bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
   switch (tile) {
-    case 0: launch_tile<128, 128, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 3: launch_tile<64, 128, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 4: launch_tile<64, 256, 1, 4, 3, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 5: launch_tile<32, 128, 1, 4, 4, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 7: launch_tile<64, 64, 2, 2, 4, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 8: launch_tile<256, 128, 4, 2, 3, EPI, GROUPED, SPARSE>(p, s); return true;
-    case 9: launch_tile<128, 256, 2, 4, 3, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 0: launch_tile<128, 128, 2, 2, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 3: launch_tile<64, 128, 2, 2, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 4: launch_tile<64, 256, 1, 4, 3, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 5: launch_tile<32, 128, 1, 4, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 7: launch_tile<64, 64, 2, 2, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 8: launch_tile<256, 128, 4, 2, 3, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 9: launch_tile<128, 256, 2, 4, 3, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 12: launch_tile<128, 128, 2, 2, 4, 32, EPI, GROUPED, SPARSE>(p, s); return true;
     default: break;
   }
   if constexpr (!GROUPED) {
     switch (tile) {
-      case 1: launch_tile<128, 256, 2, 2, 3, EPI, false, SPARSE>(p, s); return true;
-      case 2: launch_tile<256, 128, 2, 2, 3, EPI, false, SPARSE>(p, s); return true;
-      case 6: launch_tile<256, 256, 2, 4, SPARSE ? 3 : 2, EPI, false, SPARSE>(p, s); return true;
+      case 1: launch_tile<128, 256, 2, 2, 3, 16, EPI, false, SPARSE>(p, s); return true;
+      case 2: launch_tile<256, 128, 2, 2, 3, 16, EPI, false, SPARSE>(p, s); return true;
+      case 6: launch_tile<256, 256, 2, 4, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
+      case 10: launch_tile<256, 256, 4, 2, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
+      case 11: launch_tile<256, 128, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
+      case 13: launch_tile<128, 256, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
       default: break;
     }
   }

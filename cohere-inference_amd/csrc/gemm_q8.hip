@@ -86,7 +86,7 @@ int gemm_entry(GemmArgs& p, int64_t group, int64_t lda_k_req, hipStream_t s, con
                  nm + ": output rows must be aligned");
   COHERE_REQUIRE(p.epi != EPI_RESID || (aligned16(p.R) && p.ldr % 8 == 0), nm + ": residual rows must be aligned");
   if (p.M == 0) return 0;
-  p.group_steps = (int)(group / (SPARSE ? 128 : 64));
+  p.group = (int)group;
   const int tile = choose_tile(p, grouped);
   COHERE_REQUIRE(tile >= 0, nm + ": no gfx950 tile fits N=" + std::to_string(p.N));
   if (!launch_gemm<SPARSE>(tile, p.epi, grouped, p, s)) {
