@@ -16,9 +16,10 @@ executed MFMA work). The CPU baseline is the oracle's C restatement (OpenMP, all
 the same workload (dense on the pruned weights, as the CPU has no 2:4 path), next to the reference's CPU path
 (torch._int_mm) on the same sample.
 
-Extras (not the metric): config 0 (dense W8A8 5120x1280, bias) TOPS against the dense peak, and config 3's decoder-
+Extras (not the metric): config 0 (dense W8A8 5120x1280, bias) TOPS against the dense peak; config 3's decoder-
 step projections (M=64, 8 layers + head, all int8 weights) in GB/s against 8 TB/s, cold-cache (weight sets rotated so
-the 256 MB Infinity Cache cannot hold them).
+the 256 MB Infinity Cache cannot hold them); config 2's FastConformer block through the native layer loop (ms per
+block, its GEMM TOPS, and the audio-sec/sec 24 such blocks would give).
 """
 
 from __future__ import annotations
@@ -46,7 +47,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy"], default=None,
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block"], default=None,
                     help="run one part only (for rocprofv3 runs)")
     ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
     return ap.parse_args()
@@ -228,6 +229,63 @@ def decoder_extra(dev, reps_sets=4):
             "frac_of_hbm": round(bytes_step / (ms * 1e-3) / PEAK_HBM, 4)}
 
 
+def random_block(seed: int, heads: int = 16, dev=None):
+    """Config 2's FastConformer block: transformers ParakeetEncoderBlock (d_model 1280, 16 heads, FFN 5120, conv
+    kernel 9) with seeded Xavier-uniform weights, small random biases / LayerNorm affines / content and position biases
+    / BatchNorm statistics, in bf16 on the GPU. Returns (block, inv_freq)."""
+    import torch
+    from transformers.models.parakeet.configuration_parakeet import ParakeetEncoderConfig
+    from transformers.models.parakeet.modeling_parakeet import (ParakeetEncoderBlock,
+                                                                ParakeetEncoderRelPositionalEncoding)
+
+    cfg = ParakeetEncoderConfig(hidden_size=D, num_attention_heads=heads, num_key_value_heads=heads,
+                                intermediate_size=F, conv_kernel_size=9)
+    blk = ParakeetEncoderBlock(cfg, 0).eval()
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in blk.named_parameters():
+            if name.endswith(("bias_u", "bias_v")):
+                p.copy_(torch.randn(p.shape, generator=g) * 0.2)
+            elif p.dim() >= 2:
+                torch.nn.init.xavier_uniform_(p, generator=g)
+            elif "norm" in name and name.endswith("weight"):
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape, generator=g))
+            else:
+                p.copy_(0.05 * torch.randn(p.shape, generator=g))
+        bn = blk.conv.norm
+        bn.running_mean.copy_(0.05 * torch.randn(bn.running_mean.shape, generator=g))
+        bn.running_var.copy_(1.0 + 0.2 * torch.rand(bn.running_var.shape, generator=g))
+    inv_freq = ParakeetEncoderRelPositionalEncoding(cfg).inv_freq.clone()
+    return blk.to(device=dev, dtype=torch.bfloat16), inv_freq
+
+
+def block_extra(dev, replays=20):
+    """Config 2: one random-init FastConformer block (16 heads, 2:4-sparse feed-forward W2s, every linear W8A8) on
+    x (8 x 375 = 3000 packed frames, N(0,1)), through the native layer loop, in a HIP graph."""
+    import torch
+
+    from kernels.fast_encoder import EncoderLayers, metadata
+
+    blk, inv_freq = random_block(1, dev=dev)
+    layers = EncoderLayers([blk], inv_freq, sparse=True)
+    lengths = [375] * 8
+    meta = metadata(lengths, dev)
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(M, D, generator=g).to(torch.bfloat16).to(dev)
+    graph = graph_of(lambda: layers(x, lengths, meta), 1)
+    for _ in range(3):
+        graph.replay()
+    ms = time_graph(graph, replays)
+    gemm_ops = 2.0 * M * D * (4 * F + 3 * D + D + 2 * D + D)  # FF1/FF2 W1+W2, QKV, O, PW1 (GLU), PW2
+    return {"what": "config 2: one FastConformer block (d 1280, 16 heads of 80, FFN 5120 with 2:4 W2, conv module), "
+                    "all linears W8A8, 8 x 375 packed frames, native layer loop (15 launches) in a HIP graph",
+            "ms_per_block": round(ms, 4), "gemm_ops": gemm_ops,
+            "gemm_TOPS_over_block": round(gemm_ops / (ms * 1e-3) / 1e12, 1),
+            "encoder_layers_audio_sec_per_sec": round(8 * 30.0 / (24 * ms * 1e-3), 1),
+            "note": "audio-sec/sec of the 24 encoder layers alone (8 clips x 30 s through 24 such blocks); no "
+                    "front end, subsampling or decoder"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -323,6 +381,9 @@ def main():
     if not args.no_extras and args.only in (None, "decoder"):
         result["decoder_gemms"] = decoder_extra(dev)
 
+    if not args.no_extras and args.only in (None, "block"):
+        result["encoder_block"] = block_extra(dev)
+
     if args.only is not None:
         print(json.dumps(result))
         return
@@ -342,7 +403,7 @@ def main():
         "kernels_ms": result["kernels_ms"],
     }
     line["frac_of_sparse_peak"] = round(line["value"] * 1e12 / PEAK_INT8_SPARSE, 4)
-    for k in ("dense_config0", "decoder_gemms"):
+    for k in ("dense_config0", "decoder_gemms", "encoder_block"):
         if k in result:
             line[k] = result[k]
     if not args.no_cpu:

@@ -1,0 +1,390 @@
+// The FastConformer layer's non-GEMM producers on packed variable-length batches (every sequence's frames
+// concatenated, no padding), for gfx950:
+//   * the convolution module's depthwise convolution (kernel 9) + BatchNorm + SiLU, with bf16 output (reference
+//     kernels/csrc/encoder_ops.cu:455-498 dwconv_tile_kernel, 643-656) or quantized per row for the next int8 GEMM
+//     (encoder_ops.cu:559-641 dwconv_q8_kernel, 658-674);
+//   * relative-position self-attention (Transformer-XL / ParakeetEncoderAttention, encoder_ops.cu:82-337, 676-707):
+//       score[i, j] = ((q_i + u) . k_j) * scale + bf16(bf16((q_i + v) . R[i - j]) * scale)
+//     with R[d] row d + rel_off of a per-layer table of projected sinusoids, softmax over the sequence's keys, and
+//     the probabilities rounded to bf16 for the value product.
+#include "cohere_hip.h"
+#include "common.h"
+
+#include <string>
+
+namespace {
+
+// ---- depthwise convolution + BatchNorm + SiLU --------------------------------------------------------------------------
+// One workgroup holds DW_ROWS consecutive packed rows; each thread owns 8 channels, with their 9 taps, bias and
+// BatchNorm affine in registers and the DW_ROWS + 8 input rows it needs loaded once (16-byte loads). A tap reads
+// frame row + k - 4 only inside the row's own sequence [lo, hi) (zero padding at both ends of every sequence).
+// Per channel: acc = fmaf chain over the taps from the conv bias; a = bf16(acc); a = bf16(fmaf(a, bn_scale,
+// bn_shift)); y = bf16(a * sigmoid(a)). Q8 quantizes each output row with one scale (absmax / 127) instead of
+// storing bf16.
+constexpr int DW_K = 9, DW_PAD = 4, DW_ROWS = 8;
+
+DEVI float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+DEVI float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+template <bool Q8>
+__global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ cb, const float* __restrict__ bn_scale,
+                                                     const float* __restrict__ bn_shift,
+                                                     const int32_t* __restrict__ seq_lo,
+                                                     const int32_t* __restrict__ seq_hi, uint16_t* __restrict__ y,
+                                                     int8_t* __restrict__ q, float* __restrict__ qs, int rows, int C) {
+  __shared__ float red[4][DW_ROWS];
+  const int tid = threadIdx.x, c = tid * 8, r0 = blockIdx.x * DW_ROWS;
+  const bool active = c < C;
+  uint4 in[DW_ROWS + DW_K - 1];
+  float wk[8][DW_K], bias[8], sc[8], sh[8];
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < DW_ROWS + DW_K - 1; ++i) {
+      const int gr = r0 - DW_PAD + i;
+      in[i] = gr >= 0 && gr < rows ? *reinterpret_cast<const uint4*>(x + (int64_t)gr * C + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int k = 0; k < DW_K; ++k) wk[j][k] = w[(c + j) * DW_K + k];
+      bias[j] = cb[c + j];
+      sc[j] = bn_scale[c + j];
+      sh[j] = bn_shift[c + j];
+    }
+  }
+  float out[DW_ROWS][8];
+  float mx[DW_ROWS];
+#pragma unroll
+  for (int r = 0; r < DW_ROWS; ++r) {
+    const int row = r0 + r;
+    mx[r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[r][j] = 0.f;
+    if (!active || row >= rows) continue;
+    const int lo = seq_lo[row], hi = seq_hi[row];
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = bias[j];
+#pragma unroll
+    for (int k = 0; k < DW_K; ++k) {
+      const int src = row + k - DW_PAD;
+      if (src < lo || src >= hi) continue;
+      const uint32_t e[4] = {in[r + k].x, in[r + k].y, in[r + k].z, in[r + k].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv = j & 1 ? bf_hi(e[j >> 1]) : bf_lo(e[j >> 1]);
+        acc[j] = __builtin_fmaf(xv, wk[j][k], acc[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float a = round_bf(acc[j]);
+      a = round_bf(__builtin_fmaf(a, sc[j], sh[j]));
+      out[r][j] = round_bf(a * sigmoid_fast(a));
+      mx[r] = fmaxf(mx[r], fabsf(out[r][j]));
+    }
+  }
+  if constexpr (!Q8) {
+    if (!active) return;
+#pragma unroll
+    for (int r = 0; r < DW_ROWS; ++r) {
+      const int row = r0 + r;
+      if (row >= rows) break;
+      uint4 u;
+      u.x = pack_bf2(out[r][0], out[r][1]);
+      u.y = pack_bf2(out[r][2], out[r][3]);
+      u.z = pack_bf2(out[r][4], out[r][5]);
+      u.w = pack_bf2(out[r][6], out[r][7]);
+      *reinterpret_cast<uint4*>(y + (int64_t)row * C + c) = u;
+    }
+  } else {
+    const int wv = tid >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int r = 0; r < DW_ROWS; ++r) {
+      const float m = wave_max_xor(mx[r], 64);
+      if ((tid & 63) == 0) red[wv][r] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < DW_ROWS; ++r) {
+      const int row = r0 + r;
+      if (row >= rows) break;
+      float m = red[0][r];
+      for (int k = 1; k < nw; ++k) m = fmaxf(m, red[k][r]);
+      const float s = m > 0.f ? m / 127.f : 1.f, inv = 1.f / s;
+      if (active) {
+        uint32_t v[2] = {0, 0};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int qi = (int)rintf(fminf(fmaxf(out[r][k] * inv, -127.f), 127.f));
+          v[k >> 2] |= (uint32_t)(qi & 0xff) << ((k & 3) * 8);
+        }
+        *reinterpret_cast<uint2*>(q + (int64_t)row * C + c) = make_uint2(v[0], v[1]);
+      }
+      if (tid == 0) qs[row] = s;
+    }
+  }
+}
+
+// ---- relative-position self-attention ----------------------------------------------------------------------------------
+// One workgroup = one (64-query tile of one sequence, head): 4 waves of 16 queries. The matrix cores compute the
+// transposed products, so every lane owns one query (lane % 16) throughout and no probability ever moves between
+// lanes:
+//   S^T[key, q]   = K_tile (A, 16 keys x 32 dims per instruction, from LDS) . (q + u)^T (B, registers)
+//   P^T[dist, q]  = R_ring (A, 16 distances, from LDS) . (q + v)^T (B, registers)
+//   O^T[dim, q]  += V^T (A, 16 dims x 32 keys, from a transposed LDS copy of the value tile) . p^T (B, the lane's
+//                   own 8 probabilities: the 32 keys are ordered so that k slot b of lane group g is key 4g + b for
+//                   b < 4 and 16 + 4g + b - 4 after -- the same key order on both operands)
+// with v_mfma_f32_16x16x32_bf16 (lane l: row/col l % 16, k = 8 (l / 16) + b; result element e of lane l: row
+// 4 (l / 16) + e, col l % 16). Keys stream in tiles of 32 with an online softmax in fp32. The position term a key tile
+// needs spans 95 distances; each wave computes its own 48 (3 blocks of 16) from a ring of 128 table rows in LDS, of
+// which each key tile adds 32, rounds them as the module does and gathers its scores from them through a small
+// per-wave LDS buffer.
+constexpr int AT_Q = 64, AT_KEYS = 32, AT_RING = 128, AT_PW = 56;  // per-wave position buffer row (48 + pad)
+
+template <int D>
+struct AttnShape {
+  static constexpr int DP = D + 8;            // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
+  static constexpr int KS = (D + 31) / 32;    // k steps of 32 over the head size (the last one zero-padded)
+  static constexpr int OB = D / 16;           // 16-dim blocks of the output
+  static constexpr int VT = AT_KEYS + 8;      // LDS row of the transposed value tile
+  static constexpr int K_ELEMS = AT_KEYS * DP, V_ELEMS = D * VT, R_ELEMS = AT_RING * DP, P_ELEMS = 4 * 16 * AT_PW;
+  static constexpr int LDS_BYTES = 2 * (K_ELEMS + V_ELEMS + R_ELEMS + P_ELEMS);
+  static_assert(D % 16 == 0, "head size");
+};
+
+struct AttnArgs {
+  const uint16_t* qkv;  // (rows, 3 H D): q | k | v, head-major within each
+  const uint16_t* rk;   // (rel_rows, H D)
+  const uint16_t* bu;   // (H, D)
+  const uint16_t* bv;   // (H, D)
+  uint16_t* out;        // (rows, H D)
+  const int32_t* tiles; // (n, 4): sequence start, sequence length, first query row, unused
+  int H, rel_off, rel_rows;
+  float scale;
+};
+
+// 8 bf16 of an LDS row as an MFMA operand; zero past the head size (the padded last k step)
+template <int D>
+DEVI v8bf lds_op(const uint16_t* row, int col) {
+  if (D % 32 != 0 && col >= D) return v8bf{};
+  return *reinterpret_cast<const v8bf*>(row + col);
+}
+
+// bf16(q + bias) for dims col .. col + 7 of one query row (zero past the head size or for rows past the sequence)
+template <int D>
+DEVI v8bf q_plus(const uint16_t* qrow, const uint16_t* bias, int col, bool valid) {
+  if (!valid || (D % 32 != 0 && col >= D)) return v8bf{};
+  const uint4 qv = *reinterpret_cast<const uint4*>(qrow + col), bv = *reinterpret_cast<const uint4*>(bias + col);
+  const uint32_t qa[4] = {qv.x, qv.y, qv.z, qv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
+  v8bf r;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    r[2 * k] = (__bf16)(bf_lo(qa[k]) + bf_lo(ba[k]));
+    r[2 * k + 1] = (__bf16)(bf_hi(qa[k]) + bf_hi(ba[k]));
+  }
+  return r;
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) relpos_attention_kernel(const AttnArgs p) {
+  using S = AttnShape<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t lds[S::LDS_BYTES / 2];
+  uint16_t* sK = lds;                      // [32 keys][DP]
+  uint16_t* sVt = sK + S::K_ELEMS;         // [D dims][VT]
+  uint16_t* sR = sVt + S::V_ELEMS;         // [128 ring slots][DP], slot = table row & 127
+  uint16_t* sP = sR + S::R_ELEMS;          // [4 waves][16 queries][AT_PW]
+
+  const int4 tile = reinterpret_cast<const int4*>(p.tiles)[blockIdx.x];
+  const int start = tile.x, len = tile.y, q0 = tile.z, h = blockIdx.y;
+  const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), iq = lane & 15, g = lane >> 4;
+  const int HD = p.H * D, ld = 3 * HD;
+  uint16_t* sPw = sP + w * 16 * AT_PW;
+
+  // this lane's query, as the B operand of both products
+  const int qrow = q0 + 16 * w + iq;
+  const bool qvalid = qrow < len;
+  const uint16_t* qptr = p.qkv + (int64_t)(start + (qvalid ? qrow : 0)) * ld + h * D;
+  v8bf qu[S::KS], qvb[S::KS];
+#pragma unroll
+  for (int ks = 0; ks < S::KS; ++ks) {
+    qu[ks] = q_plus<D>(qptr, p.bu + h * D, ks * 32 + g * 8, qvalid);
+    qvb[ks] = q_plus<D>(qptr, p.bv + h * D, ks * 32 + g * 8, qvalid);
+  }
+
+  v4f o[S::OB];
+#pragma unroll
+  for (int i = 0; i < S::OB; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+
+  const uint16_t* kbase = p.qkv + (int64_t)start * ld + HD + h * D;
+  const uint16_t* vbase = kbase + HD;
+  constexpr int CH = D / 8;  // 16-byte chunks per row
+  for (int j0 = 0; j0 < len; j0 += AT_KEYS) {
+    // stage: keys j0 .. j0 + 31 (zero past the sequence), the value tile transposed, the new table rows. The key
+    // tile reads distances q0 - j0 - 31 .. q0 - j0 + 63; the previous tile already loaded all but the lowest 32.
+    for (int id = tid; id < AT_KEYS * CH; id += 256) {
+      const int r = id / CH, c = (id % CH) * 8, key = j0 + r;
+      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      if (key < len) {
+        kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ld + c);
+        vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * ld + c);
+      }
+      *reinterpret_cast<uint4*>(sK + r * S::DP + c) = kv;
+      const uint32_t va[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        sVt[(c + 2 * k) * S::VT + r] = (uint16_t)(va[k] & 0xffff);
+        sVt[(c + 2 * k + 1) * S::VT + r] = (uint16_t)(va[k] >> 16);
+      }
+    }
+    const int d_lo = q0 - j0 - (AT_KEYS - 1), d_hi = j0 == 0 ? q0 + AT_Q - 1 : d_lo + AT_KEYS - 1;
+    for (int id = tid; id < (d_hi - d_lo + 1) * CH; id += 256) {
+      const int d = d_lo + id / CH, c = (id % CH) * 8;
+      const int trow = min(max(d + p.rel_off, 0), p.rel_rows - 1), slot = (d + p.rel_off) & (AT_RING - 1);
+      *reinterpret_cast<uint4*>(sR + slot * S::DP + c) =
+          *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
+    }
+    __syncthreads();
+
+    // content scores of keys kb * 16 + 4 g + e for this lane's query
+    v4f s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = v4f{0.f, 0.f, 0.f, 0.f};
+      const uint16_t* krow = sK + (kb * 16 + iq) * S::DP;
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks)
+        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_op<D>(krow, ks * 32 + g * 8), qu[ks], s[kb], 0, 0, 0);
+    }
+    // position term of this wave's queries: distances dw0 + db, db < 48, rounded as the module rounds it
+    const int dw0 = q0 + 16 * w - j0 - (AT_KEYS - 1);
+#pragma unroll
+    for (int pb = 0; pb < 3; ++pb) {
+      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      const uint16_t* rrow = sR + ((dw0 + pb * 16 + iq + p.rel_off) & (AT_RING - 1)) * S::DP;
+#pragma unroll
+      for (int ks = 0; ks < S::KS; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_op<D>(rrow, ks * 32 + g * 8), qvb[ks], acc, 0, 0, 0);
+      uint2 u;
+      u.x = pack_bf2(round_bf(acc[0]) * p.scale, round_bf(acc[1]) * p.scale);
+      u.y = pack_bf2(round_bf(acc[2]) * p.scale, round_bf(acc[3]) * p.scale);
+      *reinterpret_cast<uint2*>(sPw + iq * AT_PW + pb * 16 + g * 4) = u;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's position rows, written by other lanes
+
+    // scores, masked past the sequence; online softmax per query (the 4 lane groups hold its 32 keys)
+    float sv[8], mx = m;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int jk = kb * 16 + g * 4 + e;
+        float v = -INFINITY;
+        if (j0 + jk < len) v = __builtin_fmaf(s[kb][e], p.scale, bf2f(sPw[iq * AT_PW + iq - jk + AT_KEYS - 1]));
+        sv[kb * 4 + e] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float alpha = __expf(m - mx);
+    m = mx;
+    float rs = 0.f;
+    v8bf pb;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float e = __expf(sv[k] - mx);
+      rs += e;
+      pb[k] = (__bf16)e;
+    }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l = l * alpha + rs;
+#pragma unroll
+    for (int ob = 0; ob < S::OB; ++ob) {
+      o[ob] *= alpha;
+      const uint16_t* vrow = sVt + (ob * 16 + iq) * S::VT;
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + g * 4);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + g * 4);
+      const v8bf va = __builtin_bit_cast(v8bf, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      o[ob] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[ob], 0, 0, 0);
+    }
+    __syncthreads();  // every wave is done with the key and value tiles
+  }
+
+  if (!qvalid) return;
+  const float inv = 1.f / l;
+  uint16_t* dst = p.out + (int64_t)(start + qrow) * HD + h * D;
+#pragma unroll
+  for (int ob = 0; ob < S::OB; ++ob) {
+    uint2 u;
+    u.x = pack_bf2(o[ob][0] * inv, o[ob][1] * inv);
+    u.y = pack_bf2(o[ob][2] * inv, o[ob][3] * inv);
+    *reinterpret_cast<uint2*>(dst + ob * 16 + g * 4) = u;
+  }
+}
+
+bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+template <bool Q8>
+int dwconv_entry(const uint16_t* x, const float* w, const float* cb, const float* bn_scale, const float* bn_shift,
+                 const int32_t* seq_lo, const int32_t* seq_hi, uint16_t* y, int8_t* q, float* qs, int64_t rows,
+                 int64_t C, int64_t K, void* stream, const char* name) {
+  const std::string nm(name);
+  COHERE_REQUIRE(rows >= 0 && C > 0 && C % 8 == 0 && C <= 2048, nm + ": channels must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(K == DW_K, nm + ": kernel size must be 9");
+  COHERE_REQUIRE(x && w && cb && bn_scale && bn_shift && seq_lo && seq_hi && al16(x), nm + ": bad pointer");
+  COHERE_REQUIRE(Q8 ? (q && qs && (reinterpret_cast<uintptr_t>(q) & 7) == 0) : (y && al16(y)),
+                 nm + ": bad output pointer");
+  if (rows == 0) return 0;
+  const int threads = (int)((C / 8 + 63) / 64 * 64);
+  const int grid = (int)((rows + DW_ROWS - 1) / DW_ROWS);
+  dwconv_kernel<Q8><<<grid, threads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, y, q, qs, (int)rows, (int)C);
+  return cohere::check_launch(name);
+}
+
+}  // namespace
+
+extern "C" int cohere_dwconv_bn_silu(const uint16_t* x, const float* w, const float* cb, const float* bn_scale,
+                                     const float* bn_shift, const int32_t* seq_lo, const int32_t* seq_hi, uint16_t* y,
+                                     int64_t rows, int64_t channels, int64_t ksize, void* stream) {
+  cohere::clear_error();
+  return dwconv_entry<false>(x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, y, nullptr, nullptr, rows, channels, ksize,
+                             stream, "dwconv_bn_silu");
+}
+
+extern "C" int cohere_dwconv_bn_silu_q8(const uint16_t* x, const float* w, const float* cb, const float* bn_scale,
+                                        const float* bn_shift, const int32_t* seq_lo, const int32_t* seq_hi,
+                                        int8_t* hq, float* hs, int64_t rows, int64_t channels, int64_t ksize,
+                                        void* stream) {
+  cohere::clear_error();
+  return dwconv_entry<true>(x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, nullptr, hq, hs, rows, channels, ksize,
+                            stream, "dwconv_bn_silu_q8");
+}
+
+extern "C" int cohere_relpos_attention(const uint16_t* qkv, const uint16_t* rk, int64_t rel_rows, const uint16_t* bu,
+                                       const uint16_t* bv, const int32_t* tiles, int64_t n_tiles, int64_t heads,
+                                       int64_t head_dim, int64_t rel_off, int64_t max_len, float scale, uint16_t* out,
+                                       void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(head_dim == 80 || head_dim == 160, "relpos_attention: head size must be 80 or 160");
+  COHERE_REQUIRE(heads > 0 && heads <= 65535 && n_tiles >= 0, "relpos_attention: bad sizes");
+  COHERE_REQUIRE(qkv && rk && bu && bv && tiles && out && al16(qkv) && al16(rk) && al16(bu) && al16(bv) && al16(out) &&
+                     al16(tiles),
+                 "relpos_attention: pointers must be 16-byte aligned");
+  COHERE_REQUIRE(max_len - 1 <= rel_off && rel_off + max_len + AT_Q - 2 < rel_rows,
+                 "relpos_attention: sequence too long for the distance table (" + std::to_string(max_len) + ")");
+  if (n_tiles == 0) return 0;
+  AttnArgs p;
+  p.qkv = qkv; p.rk = rk; p.bu = bu; p.bv = bv; p.out = out; p.tiles = tiles;
+  p.H = (int)heads; p.rel_off = (int)rel_off; p.rel_rows = (int)rel_rows; p.scale = scale;
+  const dim3 grid((unsigned)n_tiles, (unsigned)heads);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (head_dim == 160)
+    relpos_attention_kernel<160><<<grid, 256, 0, s>>>(p);
+  else
+    relpos_attention_kernel<80><<<grid, 256, 0, s>>>(p);
+  return cohere::check_launch("relpos_attention");
+}

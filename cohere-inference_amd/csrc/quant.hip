@@ -1,5 +1,6 @@
 // Producers of the int8 GEMM inputs: per-row activation quantization (reference kernels/csrc/encoder_ops.cu:18-54
-// store_q8 / quantize_rows) and LayerNorm(s) with int8 output (encoder_ops.cu:57-79, layernorm.cuh:6-43).
+// store_q8 / quantize_rows) and LayerNorm(s) with int8 or bf16 output (encoder_ops.cu:57-79, 501-543;
+// layernorm.cuh:6-43).
 //
 // One wave per row; each lane holds up to VEC 8-element chunks of the row in registers (16-byte loads), so a row is
 // read once and written once. The quantization arithmetic is the reference's: mx = max|bf16 x|, s = mx > 0 ?
@@ -123,11 +124,13 @@ DEVI void store_row(const Row<VEC>& r, int cols, int lane, uint16_t* x) {
   }
 }
 
-template <int VEC, bool TWO>
-__global__ void __launch_bounds__(256) layernorm_q8_kernel(uint16_t* x, int64_t ldx, const uint16_t* w1,
-                                                           const uint16_t* b1, float eps1, const uint16_t* w2,
-                                                           const uint16_t* b2, float eps2, int8_t* hq, int64_t ldq,
-                                                           float* hs, int rows, int cols) {
+// h = LN(x); with TWO, x = LN1(x) in place and h = LN2(x). Q8: h as int8 hq with one scale per row in hs;
+// otherwise h bf16 (h may be x itself: the row is in registers before anything is stored)
+template <int VEC, bool TWO, bool Q8>
+__global__ void __launch_bounds__(256) layernorm_kernel(uint16_t* x, int64_t ldx, const uint16_t* w1,
+                                                        const uint16_t* b1, float eps1, const uint16_t* w2,
+                                                        const uint16_t* b2, float eps2, int8_t* hq, int64_t ldq,
+                                                        float* hs, uint16_t* h, int64_t ldh, int rows, int cols) {
   const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
   if (row >= rows) return;
   Row<VEC> r;
@@ -138,7 +141,25 @@ __global__ void __launch_bounds__(256) layernorm_q8_kernel(uint16_t* x, int64_t 
     store_row<VEC>(r, cols, lane, xr);
     ln_row<VEC>(r, cols, lane, w2, b2, eps2);
   }
-  store_q8<VEC>(r, cols, lane, hq + (int64_t)row * ldq, hs + row);
+  if constexpr (Q8)
+    store_q8<VEC>(r, cols, lane, hq + (int64_t)row * ldq, hs + row);
+  else
+    store_row<VEC>(r, cols, lane, h + (int64_t)row * ldh);
+}
+
+template <bool Q8>
+void launch_layernorm(int vec, bool two, int grid, hipStream_t st, uint16_t* x, int64_t ldx, const uint16_t* w1,
+                      const uint16_t* b1, float eps1, const uint16_t* w2, const uint16_t* b2, float eps2, int8_t* hq,
+                      int64_t ldq, float* hs, uint16_t* h, int64_t ldh, int rows, int cols) {
+#define LNK(V, T) \
+  layernorm_kernel<V, T, Q8><<<grid, 256, 0, st>>>(x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs, h, ldh, rows, cols)
+  switch (vec) {
+    case 1: if (two) LNK(1, true); else LNK(1, false); break;
+    case 2: if (two) LNK(2, true); else LNK(2, false); break;
+    case 3: if (two) LNK(3, true); else LNK(3, false); break;
+    default: if (two) LNK(4, true); else LNK(4, false); break;
+  }
+#undef LNK
 }
 
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
@@ -178,19 +199,24 @@ extern "C" int cohere_layernorm_q8(uint16_t* x, int64_t ldx, const uint16_t* w1,
                  "layernorm_q8: rows must be aligned");
   COHERE_REQUIRE(!w2 || (b2 && al16(w2) && al16(b2)), "layernorm_q8: second LayerNorm needs aligned w2 and b2");
   if (rows == 0) return 0;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int grid = (int)((rows + 3) / 4), vec = (int)((cols + 511) / 512);
-#define LNQ(V)                                                                                                    \
-  (w2 ? layernorm_q8_kernel<V, true><<<grid, 256, 0, st>>>(x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs,     \
-                                                            (int)rows, (int)cols)                                 \
-      : layernorm_q8_kernel<V, false><<<grid, 256, 0, st>>>(x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs,    \
-                                                             (int)rows, (int)cols))
-  switch (vec) {
-    case 1: LNQ(1); break;
-    case 2: LNQ(2); break;
-    case 3: LNQ(3); break;
-    default: LNQ(4); break;
-  }
-#undef LNQ
+  launch_layernorm<true>((int)((cols + 511) / 512), w2 != nullptr, (int)((rows + 3) / 4),
+                         reinterpret_cast<hipStream_t>(stream), x, ldx, w1, b1, eps1, w2, b2, eps2, hq, ldq, hs,
+                         nullptr, 0, (int)rows, (int)cols);
   return cohere::check_launch("layernorm_q8");
+}
+
+extern "C" int cohere_layernorm(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1,
+                                const uint16_t* w2, const uint16_t* b2, float eps2, uint16_t* h, int64_t ldh,
+                                int64_t rows, int64_t cols, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && cols > 0 && cols % 8 == 0 && cols <= 2048,
+                 "layernorm: cols must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(x && w1 && b1 && h && al16(x) && ldx % 8 == 0 && al16(w1) && al16(b1) && al16(h) && ldh % 8 == 0,
+                 "layernorm: rows must be aligned");
+  COHERE_REQUIRE(!w2 || (b2 && al16(w2) && al16(b2)), "layernorm: second LayerNorm needs aligned w2 and b2");
+  if (rows == 0) return 0;
+  launch_layernorm<false>((int)((cols + 511) / 512), w2 != nullptr, (int)((rows + 3) / 4),
+                          reinterpret_cast<hipStream_t>(stream), x, ldx, w1, b1, eps1, w2, b2, eps2, nullptr, 0,
+                          nullptr, h, ldh, (int)rows, (int)cols);
+  return cohere::check_launch("layernorm");
 }

@@ -29,7 +29,8 @@ EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the 
 # every symbol include/cohere_hip.h declares
 EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_layernorm_q8", "cohere_dec_w8_linear",
            "cohere_linear_bf16", "cohere_last_error", "cohere_version", "cohere_set_gemm_tile",
-           "cohere_set_skinny_shape")
+           "cohere_set_skinny_shape", "cohere_layernorm", "cohere_dwconv_bn_silu", "cohere_dwconv_bn_silu_q8",
+           "cohere_relpos_attention", "cohere_encoder_workspace_bytes", "cohere_encoder_layers")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -47,11 +48,19 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_linear_bf16": [P, I64, P, P, P, I64, I32, I64, I64, I64, P],
         "cohere_set_gemm_tile": [I32],
         "cohere_set_skinny_shape": [I32, I32],
+        "cohere_layernorm": [P, I64, P, P, F, P, P, F, P, I64, I64, I64, P],
+        "cohere_dwconv_bn_silu": [P, P, P, P, P, P, P, P, I64, I64, I64, P],
+        "cohere_dwconv_bn_silu_q8": [P, P, P, P, P, P, P, P, P, I64, I64, I64, P],
+        "cohere_relpos_attention": [P, P, I64, P, P, P, I64, I64, I64, I64, I64, F, P, P],
+        "cohere_encoder_layers": [P, I64, P, I64, P, P, I64, P, P, I64, I64, I64, ctypes.c_double, I32, I32, I32, P,
+                                  I64, P, I64, P],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = ctypes.c_int
+    lib.cohere_encoder_workspace_bytes.argtypes = [I64, I64]
+    lib.cohere_encoder_workspace_bytes.restype = I64
     lib.cohere_last_error.restype = ctypes.c_char_p
     lib.cohere_last_error.argtypes = []
     lib.cohere_version.restype = ctypes.c_char_p
@@ -164,6 +173,86 @@ class _Ext:
         _check(hq.shape[1] == cols and hs.numel() >= rows, "layernorm_q8: shapes")
         self._call("cohere_layernorm_q8", _ptr(x), x.stride(0), _ptr(w1), _ptr(b1), float(eps1), _ptr(w2), _ptr(b2),
                    float(eps2), _ptr(hq), cols, _ptr(hs), rows, cols, _stream())
+
+    def layernorm(self, x, w1, b1, eps1, w2, b2, eps2, h):
+        """h = LN(x) in bf16; with w2: x = LN1(x) in place, h = LN2(x); h may be x (encoder_ops.cu:501-520)."""
+        _check(x.dtype == torch.bfloat16 and h.dtype == torch.bfloat16 and x.stride(1) == 1 and h.stride(1) == 1,
+               "layernorm: bf16 rows with unit column stride")
+        rows, cols = x.shape
+        _check(tuple(h.shape) == (rows, cols), "layernorm: shapes")
+        self._call("cohere_layernorm", _ptr(x), x.stride(0), _ptr(w1), _ptr(b1), float(eps1), _ptr(w2), _ptr(b2),
+                   float(eps2), _ptr(h), h.stride(0), rows, cols, _stream())
+
+    def _dwconv_checks(self, x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi):
+        _check(x.dtype == torch.bfloat16 and x.is_contiguous() and w.dtype == torch.float32 and w.is_contiguous() and
+               w.dim() == 2 and w.shape[1] == 9, "dwconv_bn_silu: contiguous bf16 x and fp32 (C, 9) weights")
+        _check(all(t.dtype == torch.float32 for t in (cb, bn_scale, bn_shift)) and
+               seq_lo.dtype == torch.int32 and seq_hi.dtype == torch.int32, "dwconv_bn_silu: dtypes")
+        _check(seq_lo.numel() >= x.shape[0] and seq_hi.numel() >= x.shape[0], "dwconv_bn_silu: lo/hi per row")
+
+    def dwconv_bn_silu(self, x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, y):
+        """y = silu(bn(depthwise conv(x))) per packed sequence, bf16 (encoder_ops.cu:643-656)."""
+        self._dwconv_checks(x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi)
+        _check(y.dtype == torch.bfloat16 and y.is_contiguous() and y.shape == x.shape, "dwconv_bn_silu: y")
+        self._call("cohere_dwconv_bn_silu", _ptr(x), _ptr(w), _ptr(cb), _ptr(bn_scale), _ptr(bn_shift), _ptr(seq_lo),
+                   _ptr(seq_hi), _ptr(y), x.shape[0], x.shape[1], w.shape[1], _stream())
+
+    def dwconv_bn_silu_q8(self, x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, hq, hs):
+        """dwconv_bn_silu with int8 rows hq and per-row scales hs (encoder_ops.cu:658-674)."""
+        self._dwconv_checks(x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi)
+        _check(hq.dtype == torch.int8 and hq.is_contiguous() and hq.shape == x.shape and hs.dtype == torch.float32 and
+               hs.numel() >= x.shape[0], "dwconv_bn_silu_q8: hq, hs")
+        self._call("cohere_dwconv_bn_silu_q8", _ptr(x), _ptr(w), _ptr(cb), _ptr(bn_scale), _ptr(bn_shift),
+                   _ptr(seq_lo), _ptr(seq_hi), _ptr(hq), _ptr(hs), x.shape[0], x.shape[1], w.shape[1], _stream())
+
+    # ---- encoder attention and layer loop (bindings.cpp:66, 85) ---------------------------------------------------
+
+    def relpos_attention(self, qkv, rk, bu, bv, tiles, rel_off, max_len, scale, out):
+        """out = relative-position self-attention of qkv per packed sequence; tiles (n, 4) int32 (sequence start,
+        length, first query row, 0) per 64-query tile (encoder_ops.cu:676-707). Head size 80 or 160."""
+        _check(qkv.is_contiguous() and out.is_contiguous() and rk.is_contiguous() and tiles.is_contiguous(),
+               "relpos_attention: contiguous tensors expected")
+        H, D = bu.shape
+        _check(bu.dtype == bv.dtype == qkv.dtype == rk.dtype == out.dtype == torch.bfloat16 and
+               tiles.dtype == torch.int32, "relpos_attention: bf16 tensors and int32 tiles")
+        _check(qkv.shape[1] == 3 * H * D and rk.shape[1] == H * D and out.shape[1] == H * D,
+               "relpos_attention: shapes")
+        self._call("cohere_relpos_attention", _ptr(qkv), _ptr(rk), rk.shape[0], _ptr(bu.contiguous()),
+                   _ptr(bv.contiguous()), _ptr(tiles), tiles.shape[0], H, D, int(rel_off), int(max_len),
+                   float(scale), _ptr(out), _stream())
+
+    def encoder_workspace_bytes(self, rows: int, group: int) -> int:
+        return int(self._lib.cohere_encoder_workspace_bytes(int(rows), int(group)))
+
+    def encoder_layers(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
+        """Every layer on packed frames x (N, 1280) bf16, in place, launched from native code
+        (kernels/csrc/encoder_loop.cpp:50-99). layers: per layer the tensors in the reference's field order
+        (fast_encoder.py:121-130); empty tensors stand for absent ones. int8 must be True."""
+        _check(bool(int8), "encoder_layers: only the int8 (W8A8) layers are provided")
+        _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.shape[1] == 1280,
+               "encoder_layers: x (N, 1280) contiguous bf16")
+        n_fields = 53
+        _check(all(len(ly) == n_fields for ly in layers), f"encoder_layers: {n_fields} tensors per layer")
+        _check(len(eps) == 5 * len(layers), "encoder_layers: 5 epsilons per layer")
+        for ly in layers:
+            for t in ly:
+                _check(t.numel() == 0 or t.is_contiguous(), "encoder_layers: layer tensors must be contiguous")
+        rows = x.shape[0]
+        cfg = [int(c) for c in cfg]
+        _check(len(cfg) >= 5, "encoder_layers: cfg needs at least 5 entries")
+        if rows == 0 or not layers:
+            return
+        H, D = layers[0][22].shape  # bias_u: (heads, head size)
+        ptrs = (ctypes.c_void_p * (n_fields * len(layers)))(
+            *[t.data_ptr() if t.numel() > 0 else None for ly in layers for t in ly])
+        eps_arr = (ctypes.c_double * len(eps))(*[float(e) for e in eps])
+        cfg_arr = (ctypes.c_int64 * len(cfg))(*cfg)
+        nbytes = self.encoder_workspace_bytes(rows, cfg[4])
+        _check(nbytes >= 0, "encoder_layers: bad feed-forward group")
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        self._call("cohere_encoder_layers", _ptr(x), rows, ptrs, len(layers), eps_arr, _ptr(tiles), tiles.shape[0],
+                   _ptr(lo), _ptr(hi), int(rel_off), int(max_len), layers[0][24].shape[0], float(scale), H, D, 1,
+                   cfg_arr, len(cfg), _ptr(ws), nbytes, _stream())
 
     # ---- decoder projections (bindings.cpp:55-56) -----------------------------------------------------------
 

@@ -1,10 +1,14 @@
-"""Encoder-side int8 linears on gfx950: the weight quantization, tile-config surface and W8A8 / 2:4 linear helpers of
+"""Encoder-side int8 path on gfx950: the weight quantization, tile-config surface and W8A8 / 2:4 linear helpers of
 the reference's kernels/fast_encoder.py (quantize_rows 60-63, I8_* / I8_SMALL / SP_CONFIGS 34-57, i8_config 50-57),
-over the HIP GEMMs of cohere-inference_amd/csrc/gemm_q8.hip.
+and its layer loop (_Layer 66-131, the distance table 155-162, metadata 203-213, layers_forward 215-226) over the HIP
+kernels of cohere-inference_amd/csrc (int8 GEMMs, attention, depthwise convolution, LayerNorms).
 
     q, s = quantize_rows(w_bf16)                         # int8 (N, K), fp32 (N)
     lin = Int8Linear(w_bf16, bias, sparse=True)          # pruned 2:4 before quantization, compressed
     y = lin(xq, xs, epi=EPI_BIAS)                        # bf16 (M, N)
+
+    layers = EncoderLayers(hf_blocks, inv_freq, sparse=True)  # transformers ParakeetEncoderBlock modules, bf16 on GPU
+    x = layers(x, lengths)                               # packed frames (sum(lengths), 1280) bf16, in place
 """
 
 from __future__ import annotations
@@ -81,5 +85,129 @@ class Int8Linear:
         return out
 
 
-__all__ = ["EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
+# ---- the layer loop --------------------------------------------------------------------------------------------------
+
+# a layer's tensors in the reference's field order (kernels/csrc/encoder_loop.cpp:34-44, fast_encoder.py:121-130)
+LAYER_FIELDS = (
+    "ln_ff1_w", "ln_ff1_b", "ln_att_w", "ln_att_b", "ln_conv_w", "ln_conv_b", "ln_ff2_w", "ln_ff2_b", "ln_out_w",
+    "ln_out_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2", "wqkv", "bqkv", "wo",
+    "bo", "bu", "bv", "rk", "wpw1", "bpw1", "wdw", "bdw", "bn_scale", "bn_shift", "wpw2", "bpw2", "q_ff1_w1",
+    "q_ff1_s1", "q_ff1_w2", "q_ff1_s2", "q_ff2_w1", "q_ff2_s1", "q_ff2_w2", "q_ff2_s2", "q_qkv_w", "q_qkv_s",
+    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e")
+GEMM_CFG = 8  # the reference's bf16 GEMM config id (its first cfg entry; unused on the int8 path)
+MAX_LEN = 512  # encoder frames the distance table covers (reference fast_encoder.py:135)
+
+
+def relative_table(inv_freq: torch.Tensor, relative_k_proj_weight: torch.Tensor, max_len: int = MAX_LEN):
+    """The per-layer table of projected sinusoids of relative distances d = -(max_len-1) .. max_len+63, row
+    d + max_len - 1: sin/cos interleaved as ParakeetEncoderRelPositionalEncoding, in the weights' dtype, then
+    projected by the layer's relative_k_proj (reference fast_encoder.py:155-162)."""
+    dev = relative_k_proj_weight.device
+    d = torch.arange(-(max_len - 1), max_len + 64, device=dev, dtype=torch.float)
+    freqs = d[:, None] * inv_freq.to(dev, torch.float)
+    pos = torch.stack([freqs.sin(), freqs.cos()], -1).reshape(len(d), -1).to(relative_k_proj_weight.dtype)
+    return torch.nn.functional.linear(pos, relative_k_proj_weight).contiguous()
+
+
+class EncoderLayer:
+    """One FastConformer block's tensors for the int8 layer loop (reference fast_encoder.py:66-131, int8 only): every
+    linear W8A8 per output channel; with sparse, the feed-forwards' second linears pruned 2:4 by magnitude (a no-op on
+    weights that already are) before quantization and stored compressed, their dense form dropped."""
+
+    def __init__(self, blk, rk: torch.Tensor, sparse: bool = False):
+        t = {}
+        ln = lambda m: (m.weight.contiguous(), m.bias.contiguous(), m.eps)  # noqa: E731
+        lns = (blk.norm_feed_forward1, blk.norm_self_att, blk.norm_conv, blk.norm_feed_forward2, blk.norm_out)
+        self.eps = []
+        for name, m in zip(("ff1", "att", "conv", "ff2", "out"), lns):
+            t[f"ln_{name}_w"], t[f"ln_{name}_b"], e = ln(m)
+            self.eps.append(float(e))
+        empty_bf = torch.empty(0, device=rk.device, dtype=rk.dtype)
+        empty_i8 = torch.empty(0, device=rk.device, dtype=torch.int8)
+        at, cv = blk.self_attn, blk.conv
+        c = cv.depthwise_conv.in_channels
+        w1, b1 = cv.pointwise_conv1.weight[:, :, 0], cv.pointwise_conv1.bias
+        wpw1 = torch.stack([w1[:c], w1[c:]], 1).reshape(2 * c, -1)  # GLU halves interleaved (a_0, g_0, a_1, ...)
+        bpw1 = torch.stack([b1[:c], b1[c:]], 1).reshape(2 * c)
+        bn = cv.norm
+        scale = bn.weight.float() / torch.sqrt(bn.running_var.float() + bn.eps)
+        for k, ff in (("ff1", blk.feed_forward1), ("ff2", blk.feed_forward2)):
+            t[f"{k}_w1"], t[f"{k}_w2"] = empty_bf, empty_bf
+            t[f"{k}_b1"], t[f"{k}_b2"] = ff.linear1.bias.contiguous(), ff.linear2.bias.contiguous()
+            t[f"q_{k}_w1"], t[f"q_{k}_s1"] = quantize_rows(ff.linear1.weight)
+            w2 = prune_24_magnitude(ff.linear2.weight) if sparse else ff.linear2.weight
+            t[f"q_{k}_w2"], t[f"q_{k}_s2"] = quantize_rows(w2)
+            if sparse:
+                t[f"sp_{k}_w"], t[f"sp_{k}_e"] = compress_24(t[f"q_{k}_w2"])
+                t[f"q_{k}_w2"] = empty_i8
+            else:
+                t[f"sp_{k}_w"], t[f"sp_{k}_e"] = empty_i8, empty_i8.int()
+        wqkv = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight])
+        t["bqkv"] = torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias]).contiguous()
+        t["wqkv"] = t["wo"] = t["wpw1"] = t["wpw2"] = empty_bf
+        t["bo"], t["bu"], t["bv"], t["rk"] = (at.o_proj.bias.contiguous(), at.bias_u.contiguous(),
+                                              at.bias_v.contiguous(), rk)
+        t["bpw1"] = bpw1.contiguous()
+        t["wdw"] = cv.depthwise_conv.weight[:, 0, :].float().contiguous()
+        t["bdw"] = cv.depthwise_conv.bias.float().contiguous()
+        t["bn_scale"] = scale.contiguous()
+        t["bn_shift"] = (bn.bias.float() - bn.running_mean.float() * scale).contiguous()
+        t["bpw2"] = cv.pointwise_conv2.bias.contiguous()
+        t["q_qkv_w"], t["q_qkv_s"] = quantize_rows(wqkv)
+        t["q_pw1_w"], t["q_pw1_s"] = quantize_rows(wpw1)
+        t["q_o_w"], t["q_o_s"] = quantize_rows(at.o_proj.weight)
+        t["q_pw2_w"], t["q_pw2_s"] = quantize_rows(cv.pointwise_conv2.weight[:, :, 0])
+        self.tensors = t
+        self.heads, self.head_dim = at.bias_u.shape
+
+    def fields(self) -> list[torch.Tensor]:
+        """This layer's tensors in the reference's field order."""
+        return [self.tensors[k] for k in LAYER_FIELDS]
+
+
+def metadata(lengths: list[int], device) -> dict:
+    """The packed batch's attention tiles (sequence start, length, first query row, 0) per 64 queries, and each row's
+    sequence range [lo, hi) for the depthwise convolution (reference fast_encoder.py:203-213)."""
+    starts, s = [], 0
+    for n in lengths:
+        starts.append(s)
+        s += n
+    tiles = [(st, n, q0, 0) for st, n in zip(starts, lengths) for q0 in range(0, n, 64)]
+    lo = torch.tensor([st for st, n in zip(starts, lengths) for _ in range(n)], dtype=torch.int32)
+    hi = torch.tensor([st + n for st, n in zip(starts, lengths) for _ in range(n)], dtype=torch.int32)
+    return {"tiles": torch.tensor(tiles, dtype=torch.int32).reshape(-1, 4).to(device),
+            "lo": lo.to(device), "hi": hi.to(device), "max_len": max(lengths) if lengths else 0}
+
+
+class EncoderLayers:
+    """The int8 layers of a FastConformer encoder on packed frames (reference FastEncoder.layers_forward,
+    fast_encoder.py:215-226): blocks are transformers ParakeetEncoderBlock modules (1280 wide, 8 or 16 heads) whose
+    weights are converted once; a call runs every layer through ext.encoder_layers, one native launch loop."""
+
+    def __init__(self, blocks, inv_freq: torch.Tensor, sparse: bool = False, max_len: int = MAX_LEN):
+        with torch.no_grad():
+            self.layers = [EncoderLayer(b, relative_table(inv_freq, b.self_attn.relative_k_proj.weight, max_len),
+                                        sparse) for b in blocks]
+        self.layer_tensors = [ly.fields() for ly in self.layers]
+        self.layer_eps = [e for ly in self.layers for e in ly.eps]
+        self.max_len, self.rel_off = max_len, max_len - 1
+        self.scale = self.layers[0].head_dim ** -0.5
+        self.sparse = sparse
+
+    def configs(self, n: int) -> list[int]:
+        return [GEMM_CFG, i8_config("qkv", n, I8_CFG), i8_config("ff2", n, I8_CFG_GROUPED),
+                i8_config("ff1", n, I8_CFG_FF1), FF_GROUP, i8_config("pw1", n, I8_CFG), i8_config("o", n, I8_CFG),
+                next(c for up_to, c in SP_CONFIGS if n <= up_to)]
+
+    @torch.no_grad()
+    def __call__(self, x: torch.Tensor, lengths: list[int], meta: dict | None = None) -> torch.Tensor:
+        meta = metadata(lengths, x.device) if meta is None else meta
+        if meta["max_len"] > self.max_len:
+            raise RuntimeError(f"encoder_layers: sequence of {meta['max_len']} frames exceeds {self.max_len}")
+        ext.encoder_layers(x, self.layer_tensors, self.layer_eps, meta["tiles"], meta["lo"], meta["hi"], self.rel_off,
+                           meta["max_len"], self.scale, True, self.configs(x.shape[0]))
+        return x
+
+
+__all__ = ["EncoderLayer", "EncoderLayers", "LAYER_FIELDS", "metadata", "relative_table", "EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
            "I8_SMALL", "SP_CONFIGS", "Int8Linear", "i8_config", "quantize_activations", "quantize_rows"]

@@ -33,7 +33,7 @@ enum {
   COHERE_EPI_I32 = 7
 };
 
-/* Replaces gemm_i8 (reference kernels/csrc/gemm_int8.cu:351-391, bound at kernels/csrc/bindings.cpp:66).
+/* Replaces gemm_i8 (reference kernels/csrc/gemm_int8.cu:351-391, bound at kernels/csrc/bindings.cpp:67).
  * out = epilogue(dequant(a @ w^T) + bias): a int8 [M, K] (lda), sa fp32 [M, K / group] (ldsa), w int8 [N, K]
  * contiguous, sw fp32 [N], bias bf16 [N] or NULL.
  *   BIAS     out bf16 [M, N]
@@ -49,7 +49,7 @@ int cohere_gemm_i8(const int8_t* a, int64_t lda, const float* sa, int64_t ldsa, 
                    int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N, int64_t K, int32_t cfg,
                    void* stream);
 
-/* Replaces gemm_sp (reference kernels/csrc/gemm_sparse.cu:214-253, bound at kernels/csrc/bindings.cpp:84) and
+/* Replaces gemm_sp (reference kernels/csrc/gemm_sparse.cu:214-253, bound at kernels/csrc/bindings.cpp:68) and
  * widens it to gemm_i8's epilogues. x int8 [M, K] (ldx) with sx fp32 [M, K / group] (ldsx); the 2:4 weights as
  * kernels/sparse.py compress_24 stores them: wc int8 [N, K / 2] kept values, e int32 [N, K / 32] selectors (a nibble
  * i0 | i1 << 2 per group of four, lowest K in the lowest nibble) -- exactly the CDNA4 SMFMAC A operand and index
@@ -61,13 +61,13 @@ int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, 
                    const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N,
                    int64_t K, int32_t cfg, void* stream);
 
-/* Replaces quantize_rows (reference kernels/csrc/encoder_ops.cu:545-553, bound at bindings.cpp:70): bf16 rows x
+/* Replaces quantize_rows (reference kernels/csrc/encoder_ops.cu:545-553, bound at bindings.cpp:69): bf16 rows x
  * [rows, cols] (ldx) -> int8 q [rows, cols] (ldq) and fp32 s [rows]; one scale per row, absmax / 127;
  * cols % 8 == 0, cols <= 8192. */
 int cohere_quantize_rows(const uint16_t* x, int64_t ldx, int8_t* q, int64_t ldq, float* s, int64_t rows, int64_t cols,
                          void* stream);
 
-/* Replaces layernorm_q8 (reference kernels/csrc/encoder_ops.cu:522-543, bound at bindings.cpp:71): h = LN(x) as int8
+/* Replaces layernorm_q8 (reference kernels/csrc/encoder_ops.cu:522-543, bound at bindings.cpp:70): h = LN(x) as int8
  * hq with per-row scale hs; with w2 != NULL, x = LN1(x) in place and h = LN2(x). bf16 x [rows, cols] (ldx),
  * weights/biases bf16 [cols]. */
 int cohere_layernorm_q8(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1,
@@ -90,6 +90,60 @@ int cohere_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_t* w, const
  * M <= 64, fp32 accumulation; N % 16 == 0, K % 64 == 0. */
 int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
                        int64_t ldy, int32_t relu, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Replaces layernorm (reference kernels/csrc/encoder_ops.cu:501-520, bound at kernels/csrc/bindings.cpp:73):
+ * h = LN1(x) as bf16; with w2 (non-NULL), x = LN1(x) in place and h = LN2(x). h may be x. fp32 statistics, the
+ * result rounded to bf16. cols % 8 == 0, cols <= 2048. */
+int cohere_layernorm(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1, const uint16_t* w2,
+                     const uint16_t* b2, float eps2, uint16_t* h, int64_t ldh, int64_t rows, int64_t cols,
+                     void* stream);
+
+/* Replaces dwconv_bn_silu (reference kernels/csrc/encoder_ops.cu:643-656, bound at kernels/csrc/bindings.cpp:74):
+ * y = bf16(silu(bf16(bn(bf16(dwconv(x)))))) per packed row: x, y bf16 [rows, channels] contiguous; w fp32
+ * [channels, 9]; cb, bn_scale, bn_shift fp32 [channels]; seq_lo / seq_hi int32 [rows], the packed-row range of each
+ * row's own sequence (taps outside it read zero). channels % 8 == 0, <= 2048; ksize must be 9. */
+int cohere_dwconv_bn_silu(const uint16_t* x, const float* w, const float* cb, const float* bn_scale,
+                          const float* bn_shift, const int32_t* seq_lo, const int32_t* seq_hi, uint16_t* y,
+                          int64_t rows, int64_t channels, int64_t ksize, void* stream);
+
+/* Replaces dwconv_bn_silu_q8 (reference kernels/csrc/encoder_ops.cu:658-674, bound at kernels/csrc/bindings.cpp:75):
+ * as cohere_dwconv_bn_silu, the rows written as int8 hq [rows, channels] with one fp32 scale per row hs [rows]
+ * (absmax / 127, the arithmetic of cohere_quantize_rows). */
+int cohere_dwconv_bn_silu_q8(const uint16_t* x, const float* w, const float* cb, const float* bn_scale,
+                             const float* bn_shift, const int32_t* seq_lo, const int32_t* seq_hi, int8_t* hq,
+                             float* hs, int64_t rows, int64_t channels, int64_t ksize, void* stream);
+
+/* Replaces relpos_attention (reference kernels/csrc/encoder_ops.cu:676-707, bound at kernels/csrc/bindings.cpp:85).
+ * out [rows, H D] bf16 = relative-position self-attention of qkv [rows, 3 H D] bf16 (q | k | v) within each
+ * sequence: score[i, j] = ((q_i + bu) . k_j) scale + bf16(bf16((q_i + bv) . rk[i - j + rel_off]) scale), softmax
+ * over the sequence's keys, probabilities rounded to bf16 for the value product. rk [rel_rows, H D] bf16, bu / bv
+ * [H, D] bf16; tiles int32 [n_tiles, 4] = (sequence start row, sequence length, first query row, 0) for every
+ * 64-query tile of every sequence. Head size D = 80 or 160 (the reference: 160 only). Rejects
+ * max_len - 1 > rel_off or rel_off + max_len + 62 >= rel_rows, as the reference does. */
+int cohere_relpos_attention(const uint16_t* qkv, const uint16_t* rk, int64_t rel_rows, const uint16_t* bu,
+                            const uint16_t* bv, const int32_t* tiles, int64_t n_tiles, int64_t heads, int64_t head_dim,
+                            int64_t rel_off, int64_t max_len, float scale, uint16_t* out, void* stream);
+
+/* Number of per-layer tensors of cohere_encoder_layers (the reference's enum F, kernels/csrc/encoder_loop.cpp:34-44) */
+enum { COHERE_ENC_N_FIELDS = 53 };
+
+/* Device bytes cohere_encoder_layers needs as workspace for `rows` packed frames and feed-forward scale group
+ * `group` (-1 on bad arguments). The reference allocates the same buffers inside the call. */
+int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group);
+
+/* Replaces encoder_layers, int8 branch (reference kernels/csrc/encoder_loop.cpp:50-99, bound at
+ * kernels/csrc/bindings.cpp:66): every layer of the FastConformer encoder on packed frames x [rows, 1280] bf16, in
+ * place, in the reference's launch order. fields: n_layers x COHERE_ENC_N_FIELDS device pointers in the reference's
+ * field order (NULL for the empty tensors: a dense W2 whose 2:4 form is given, the 2:4 fields of a dense layer,
+ * absent biases). eps: n_layers x 5 (ff1, att, conv, ff2, out). tiles / lo / hi / rel_off / max_len / scale as in
+ * cohere_relpos_attention and cohere_dwconv_bn_silu; rel_rows the table rows. cfg: the reference's list (bf16 config,
+ * int8 QKV, grouped FF W2, FF W1, FF group, PW1, O/PW2, 2:4 FF W2). int8 must be nonzero: the bf16 branch is not
+ * provided. workspace: at least cohere_encoder_workspace_bytes(rows, cfg[4]) bytes of device memory. */
+int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers, const double* eps,
+                          const int32_t* tiles, int64_t n_tiles, const int32_t* lo, const int32_t* hi, int64_t rel_off,
+                          int64_t max_len, int64_t rel_rows, double scale, int32_t heads, int32_t head_dim,
+                          int32_t int8, const int64_t* cfg, int64_t n_cfg, void* workspace, int64_t workspace_bytes,
+                          void* stream);
 
 /* The last error on this thread ("" when none). */
 const char* cohere_last_error(void);

@@ -22,6 +22,14 @@ Function -> reference -> what pins it (tests/test_oracle.py unless noted):
   prepare_w8            kernels/stream_decoder.py:38-48  un-permute + dequantize == quantize_weight_rows
   dec_w8_linear         kernels/csrc/dec_w8.cu:46-180    torch float64 matmul of the dequantized weights
   linear_bf16           kernels/decoder_kernels.py:19-34 torch float64 matmul
+  layernorm             kernels/csrc/layernorm.cuh:6-43  torch.nn.functional.layer_norm in float64
+  dwconv_bn_silu        kernels/csrc/encoder_ops.cu:455-498, 559-641  torch conv1d (groups = channels) per sequence
+                                                        in float64, then BatchNorm and SiLU
+  relpos_attention      kernels/csrc/encoder_ops.cu:82-337  transformers' ParakeetEncoderAttention (rel_shift form)
+                                                        in float32; with a zero table and zero biases, softmax
+                                                        attention in float64
+  encoder_layers_int8   kernels/csrc/encoder_loop.cpp:63-99  transformers' ParakeetEncoderBlock in float32 on the
+                                                        dequantized weights (within the int8 activation error)
 """
 
 from __future__ import annotations
@@ -56,6 +64,9 @@ def lib() -> ctypes.CDLL:
         i64, p = ctypes.c_int64, ctypes.c_void_p
         _lib.orc_quantize_weight_rows.argtypes = [p, i64, i64, p, p]
         _lib.orc_q8_rows.argtypes = [p, i64, i64, i64, p, i64, p]
+        _lib.orc_layernorm.argtypes = [p, i64, p, p, ctypes.c_float, p, p, ctypes.c_float, p, i64, i64, i64]
+        _lib.orc_dwconv_bn_silu.argtypes = [p, p, p, p, p, p, p, p, i64, i64]
+        _lib.orc_relpos_attention.argtypes = [p, p, i64, p, p, p, p, i64, i64, i64, i64, ctypes.c_float, p]
         _lib.orc_gemm_i8.argtypes = [p, i64, p, i64, i64, p, i64, p, p, p, i64, ctypes.c_int, p, i64, ctypes.c_float,
                                      p, i64, i64, i64, i64, i64, p, ctypes.c_int]
         _lib.orc_gemm_i8.restype = ctypes.c_int
@@ -220,3 +231,102 @@ def linear_bf16(x, w, bias, relu=False, threads=0):
     y = np.empty((M, N), np.uint16)
     lib().orc_linear_bf16(_p(x), K, _p(w), _p(bias), _p(y), N, int(relu), M, N, K, threads)
     return y
+
+
+# ---- the encoder layer's other producers and the layer loop (row a9) ------------------------------------------------
+
+def layernorm(x, w1, b1, eps1, w2=None, b2=None, eps2=0.0):
+    """layernorm.cuh:6-43: returns (h, x') as bf16 bits; x' = LN1(x) when w2 is given (else x unchanged)."""
+    x = _c(x, np.uint16).copy()
+    rows, cols = x.shape
+    h = np.empty_like(x)
+    lib().orc_layernorm(_p(x), cols, _p(_c(w1, np.uint16)), _p(_c(b1, np.uint16)), eps1,
+                        _p(None if w2 is None else _c(w2, np.uint16)), _p(None if b2 is None else _c(b2, np.uint16)),
+                        eps2, _p(h), cols, rows, cols)
+    return h, x
+
+
+def dwconv_bn_silu(x, w, cb, bn_scale, bn_shift, lo, hi):
+    """encoder_ops.cu:455-498: bf16 bits [rows, C] -> bf16 bits [rows, C]."""
+    x = _c(x, np.uint16)
+    rows, C = x.shape
+    y = np.empty_like(x)
+    lib().orc_dwconv_bn_silu(_p(x), _p(_c(w, np.float32)), _p(_c(cb, np.float32)), _p(_c(bn_scale, np.float32)),
+                             _p(_c(bn_shift, np.float32)), _p(_c(lo, np.int32)), _p(_c(hi, np.int32)), _p(y), rows, C)
+    return y
+
+
+def dwconv_bn_silu_q8(x, w, cb, bn_scale, bn_shift, lo, hi):
+    """encoder_ops.cu:559-641: the rows of dwconv_bn_silu quantized (store_q8's arithmetic)."""
+    return q8_rows(dwconv_bn_silu(x, w, cb, bn_scale, bn_shift, lo, hi))
+
+
+def relpos_attention(qkv, rk, bu, bv, lengths, rel_off, scale):
+    """encoder_ops.cu:82-337 over packed sequences of the given lengths: bf16 bits [rows, H D]."""
+    qkv, rk = _c(qkv, np.uint16), _c(rk, np.uint16)
+    bu, bv = _c(bu, np.uint16), _c(bv, np.uint16)
+    H, D = bu.shape
+    lengths = np.asarray(lengths, np.int32)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int32)
+    out = np.zeros((qkv.shape[0], H * D), np.uint16)
+    lib().orc_relpos_attention(_p(qkv), _p(rk), rk.shape[0], _p(bu), _p(bv), _p(starts), _p(lengths), len(lengths),
+                               H, D, rel_off, scale, _p(out))
+    return out
+
+
+# the reference's per-layer field order (kernels/csrc/encoder_loop.cpp:34-44)
+LAYER_FIELDS = (
+    "ln_ff1_w", "ln_ff1_b", "ln_att_w", "ln_att_b", "ln_conv_w", "ln_conv_b", "ln_ff2_w", "ln_ff2_b", "ln_out_w",
+    "ln_out_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2", "wqkv", "bqkv", "wo",
+    "bo", "bu", "bv", "rk", "wpw1", "bpw1", "wdw", "bdw", "bn_scale", "bn_shift", "wpw2", "bpw2", "q_ff1_w1",
+    "q_ff1_s1", "q_ff1_w2", "q_ff1_s2", "q_ff2_w1", "q_ff2_s1", "q_ff2_w2", "q_ff2_s2", "q_qkv_w", "q_qkv_s",
+    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e")
+
+
+def encoder_layers_int8(x, layers, eps, lengths, rel_off, scale, group=256, qgroup_ff1=256, threads=0):
+    """encoder_loop.cpp:63-99 (the int8 branch), each step by the functions above and gemm_i8: x bf16 bits
+    [rows, 1280] -> the layers' output (bf16 bits). layers: one dict per layer, LAYER_FIELDS -> numpy arrays (bf16 as
+    uint16 bits; the 2:4 W2 given as sp_ff*_w/e is run as the dense GEMM on its decompressed weights, which is
+    gemm_sparse.cu's result bit for bit). eps: per layer (ff1, att, conv, ff2, out)."""
+    x = _c(x, np.uint16).copy()
+    lengths = list(lengths)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    lo = np.concatenate([np.full(n, s) for s, n in zip(starts, lengths)]).astype(np.int32)
+    hi = np.concatenate([np.full(n, s + n) for s, n in zip(starts, lengths)]).astype(np.int32)
+
+    def ffn(ly, hq, hs, k):
+        tq, ts = gemm_i8(hq, hs, hq.shape[1], ly[f"q_ff{k}_w1"], ly[f"q_ff{k}_s1"], ly.get(f"ff{k}_b1"), EPI_SILU_Q8,
+                         qgroup=qgroup_ff1, threads=threads)
+        sp = ly.get(f"sp_ff{k}_w")
+        w2 = decompress_24(sp, ly[f"sp_ff{k}_e"]) if sp is not None and sp.size else ly[f"q_ff{k}_w2"]
+        return gemm_i8(tq, ts, group, w2, ly[f"q_ff{k}_s2"], ly.get(f"ff{k}_b2"), EPI_RESID, resid=x, alpha=0.5,
+                       threads=threads)
+
+    L = len(layers)
+    h, _ = layernorm(x, layers[0]["ln_ff1_w"], layers[0]["ln_ff1_b"], eps[0][0])
+    hq, hs = q8_rows(h)
+    for i, ly in enumerate(layers):
+        x = ffn(ly, hq, hs, 1)
+        h, _ = layernorm(x, ly["ln_att_w"], ly["ln_att_b"], eps[i][1])
+        hq, hs = q8_rows(h)
+        qkv = gemm_i8(hq, hs, hq.shape[1], ly["q_qkv_w"], ly["q_qkv_s"], ly.get("bqkv"), EPI_BIAS, threads=threads)
+        a = relpos_attention(qkv, ly["rk"], ly["bu"], ly["bv"], lengths, rel_off, scale)
+        hq, hs = q8_rows(a)
+        x = gemm_i8(hq, hs, hq.shape[1], ly["q_o_w"], ly["q_o_s"], ly.get("bo"), EPI_RESID, resid=x, alpha=1.0,
+                    threads=threads)
+        h, _ = layernorm(x, ly["ln_conv_w"], ly["ln_conv_b"], eps[i][2])
+        hq, hs = q8_rows(h)
+        a = gemm_i8(hq, hs, hq.shape[1], ly["q_pw1_w"], ly["q_pw1_s"], ly.get("bpw1"), EPI_GLU, threads=threads)
+        hq, hs = dwconv_bn_silu_q8(a, ly["wdw"], ly["bdw"], ly["bn_scale"], ly["bn_shift"], lo, hi)
+        x = gemm_i8(hq, hs, hq.shape[1], ly["q_pw2_w"], ly["q_pw2_s"], ly.get("bpw2"), EPI_RESID, resid=x, alpha=1.0,
+                    threads=threads)
+        h, _ = layernorm(x, ly["ln_ff2_w"], ly["ln_ff2_b"], eps[i][3])
+        hq, hs = q8_rows(h)
+        x = ffn(ly, hq, hs, 2)
+        if i + 1 < L:
+            h, x = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4], layers[i + 1]["ln_ff1_w"],
+                             layers[i + 1]["ln_ff1_b"], eps[i + 1][0])
+            hq, hs = q8_rows(h)
+        else:
+            x, _ = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4])
+    return x

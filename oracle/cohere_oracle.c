@@ -289,6 +289,126 @@ void orc_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const ui
     }
 }
 
+/* ---- the encoder layer's other producers (row a9's launch loop) ---------------------------------------------- */
+
+/* kernels/csrc/layernorm.cuh:6-43 + encoder_ops.cu:57-79: h = bf16(fmaf((x - mean) * rstd, w, b)) with fp32
+ * statistics over the bf16 row (here accumulated in fp64 and rounded to fp32 once; the kernel's warp tree sums in
+ * fp32), rstd = 1 / sqrt(var + eps). With w2: x = LN1(x) in place, then h = LN2(x). h may alias x. */
+static void ln_row(const float* v, int64_t cols, const uint16_t* w, const uint16_t* b, float eps, float* out) {
+  double s = 0.0;
+  for (int64_t k = 0; k < cols; ++k) s += v[k];
+  const float mean = (float)(s / (double)cols);
+  double q = 0.0;
+  for (int64_t k = 0; k < cols; ++k) {
+    const float d = v[k] - mean;
+    q += (double)d * (double)d;
+  }
+  const float rstd = 1.f / sqrtf((float)(q / (double)cols) + eps);
+  for (int64_t k = 0; k < cols; ++k) out[k] = round_bf(fmaf((v[k] - mean) * rstd, bf2f(w[k]), bf2f(b[k])));
+}
+
+void orc_layernorm(uint16_t* x, int64_t ldx, const uint16_t* w1, const uint16_t* b1, float eps1, const uint16_t* w2,
+                   const uint16_t* b2, float eps2, uint16_t* h, int64_t ldh, int64_t rows, int64_t cols) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    float* v = (float*)malloc(sizeof(float) * cols * 2);
+    float* o = v + cols;
+    for (int64_t k = 0; k < cols; ++k) v[k] = bf2f(x[r * ldx + k]);
+    ln_row(v, cols, w1, b1, eps1, o);
+    if (w2) {
+      for (int64_t k = 0; k < cols; ++k) x[r * ldx + k] = f2bf(o[k]);
+      memcpy(v, o, sizeof(float) * cols);
+      ln_row(v, cols, w2, b2, eps2, o);
+    }
+    for (int64_t k = 0; k < cols; ++k) h[r * ldh + k] = f2bf(o[k]);
+    free(v);
+  }
+}
+
+/* kernels/csrc/encoder_ops.cu:455-498 (dwconv_tile_kernel) and 559-641 (dwconv_q8_kernel, whose int8 rows are
+ * q8_rows of this output): per channel c of row r, acc = cb[c], then for taps k = 0..8 in order, for source row
+ * src = r + k - 4 inside [lo[r], hi[r]): acc = fmaf(x[src, c], w[c, k], acc); a = bf16(acc);
+ * a = bf16(fmaf(a, bn_scale[c], bn_shift[c])); y = bf16(a * sigmoid(a)). */
+void orc_dwconv_bn_silu(const uint16_t* x, const float* w, const float* cb, const float* bn_scale,
+                        const float* bn_shift, const int32_t* lo, const int32_t* hi, uint16_t* y, int64_t rows,
+                        int64_t C) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t c = 0; c < C; ++c) {
+      float acc = cb[c];
+      for (int k = 0; k < 9; ++k) {
+        const int64_t src = r + k - 4;
+        if (src < lo[r] || src >= hi[r]) continue;
+        acc = fmaf(bf2f(x[src * C + c]), w[c * 9 + k], acc);
+      }
+      float a = round_bf(acc);
+      a = round_bf(fmaf(a, bn_scale[c], bn_shift[c]));
+      y[r * C + c] = f2bf(a * sigmoid(a));
+    }
+}
+
+/* kernels/csrc/encoder_ops.cu:82-337 relpos_attention_kernel, for each (sequence, head, query i):
+ *   qu = bf16(q_i + u), qv = bf16(q_i + v) (fp32 adds);
+ *   s_j = fmaf(qu . k_j, scale, bf16(bf16(qv . R[clamp(i - j + rel_off)]) * scale)) for keys j of the sequence;
+ *   keys in tiles of 32 with the online softmax of the kernel: m' = max(m, max_j s_j), alpha = exp(m - m'),
+ *   p_j = exp(s_j - m'), l = l * alpha + sum p_j, o = o * alpha + sum bf16(p_j) v_j; out = bf16(o * (1 / l)).
+ * Dot products in fp64, rounded to fp32 once (the kernel accumulates fp32 on the tensor cores). */
+void orc_relpos_attention(const uint16_t* qkv, const uint16_t* rk, int64_t rel_rows, const uint16_t* bu,
+                          const uint16_t* bv, const int32_t* seq_start, const int32_t* seq_len, int64_t n_seq,
+                          int64_t H, int64_t D, int64_t rel_off, float scale, uint16_t* out) {
+  const int64_t HD = H * D, ld = 3 * HD;
+  for (int64_t sq = 0; sq < n_seq; ++sq) {
+    const int64_t start = seq_start[sq], len = seq_len[sq];
+#pragma omp parallel for collapse(2) schedule(dynamic)
+    for (int64_t h = 0; h < H; ++h)
+      for (int64_t i = 0; i < len; ++i) {
+        float* buf = (float*)malloc(sizeof(float) * (3 * D + 32));
+        float *qu = buf, *qv = buf + D, *o = buf + 2 * D, *sv = buf + 3 * D;
+        const uint16_t* q = qkv + (start + i) * ld + h * D;
+        for (int64_t d = 0; d < D; ++d) {
+          qu[d] = round_bf(bf2f(q[d]) + bf2f(bu[h * D + d]));
+          qv[d] = round_bf(bf2f(q[d]) + bf2f(bv[h * D + d]));
+          o[d] = 0.f;
+        }
+        float m = -INFINITY, l = 0.f;
+        for (int64_t j0 = 0; j0 < len; j0 += 32) {
+          const int64_t jn = len - j0 < 32 ? len - j0 : 32;
+          float mx = m;
+          for (int64_t jj = 0; jj < jn; ++jj) {
+            const int64_t j = j0 + jj;
+            const uint16_t* k = qkv + (start + j) * ld + HD + h * D;
+            int64_t row = i - j + rel_off;
+            row = row < 0 ? 0 : (row >= rel_rows ? rel_rows - 1 : row);
+            const uint16_t* r = rk + row * HD + h * D;
+            double ac = 0.0, bd = 0.0;
+            for (int64_t d = 0; d < D; ++d) {
+              ac += (double)qu[d] * (double)bf2f(k[d]);
+              bd += (double)qv[d] * (double)bf2f(r[d]);
+            }
+            const float pos = round_bf(round_bf((float)bd) * scale);
+            sv[jj] = fmaf((float)ac, scale, pos);
+            if (sv[jj] > mx) mx = sv[jj];
+          }
+          const float alpha = expf(m - mx);
+          m = mx;
+          float rs = 0.f;
+          for (int64_t d = 0; d < D; ++d) o[d] *= alpha;
+          for (int64_t jj = 0; jj < jn; ++jj) {
+            const float p = expf(sv[jj] - mx);
+            rs += p;
+            const float pr = round_bf(p);
+            const uint16_t* v = qkv + (start + j0 + jj) * ld + 2 * HD + h * D;
+            for (int64_t d = 0; d < D; ++d) o[d] = fmaf(pr, bf2f(v[d]), o[d]);
+          }
+          l = l * alpha + rs;
+        }
+        const float inv = 1.f / l;
+        for (int64_t d = 0; d < D; ++d) out[(start + i) * HD + h * D + d] = f2bf(o[d] * inv);
+        free(buf);
+      }
+  }
+}
+
 /* bf16 <-> fp32 helpers exported for the Python side of the checker */
 void orc_f32_to_bf16(const float* f, uint16_t* h, int64_t n) {
   for (int64_t i = 0; i < n; ++i) h[i] = f2bf(f[i]);
