@@ -37,6 +37,7 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
   const int tid = threadIdx.x, c = tid * 8, r0 = blockIdx.x * DW_ROWS;
   const bool active = c < C;
   uint4 in[DW_ROWS + DW_K - 1];
+  // a thread's 8 channels x 9 taps are 72 consecutive floats of the (C, 9) layout: 18 16-byte loads
   float wk[8][DW_K], bias[8], sc[8], sh[8];
   if (active) {
 #pragma unroll
@@ -44,13 +45,15 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
       const int gr = r0 - DW_PAD + i;
       in[i] = gr >= 0 && gr < rows ? *reinterpret_cast<const uint4*>(x + (int64_t)gr * C + c) : make_uint4(0, 0, 0, 0);
     }
+    float* wf = &wk[0][0];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int v = 0; v < 8 * DW_K / 4; ++v)
+      *reinterpret_cast<float4*>(wf + 4 * v) = *reinterpret_cast<const float4*>(w + (int64_t)c * DW_K + 4 * v);
 #pragma unroll
-      for (int k = 0; k < DW_K; ++k) wk[j][k] = w[(c + j) * DW_K + k];
-      bias[j] = cb[c + j];
-      sc[j] = bn_scale[c + j];
-      sh[j] = bn_shift[c + j];
+    for (int j = 0; j < 8; j += 4) {
+      *reinterpret_cast<float4*>(bias + j) = *reinterpret_cast<const float4*>(cb + c + j);
+      *reinterpret_cast<float4*>(sc + j) = *reinterpret_cast<const float4*>(bn_scale + c + j);
+      *reinterpret_cast<float4*>(sh + j) = *reinterpret_cast<const float4*>(bn_shift + c + j);
     }
   }
   float out[DW_ROWS][8];
@@ -221,32 +224,57 @@ __global__ void __launch_bounds__(256) relpos_attention_kernel(const AttnArgs p)
   const uint16_t* kbase = p.qkv + (int64_t)start * ld + HD + h * D;
   const uint16_t* vbase = kbase + HD;
   constexpr int CH = D / 8;  // 16-byte chunks per row
-  for (int j0 = 0; j0 < len; j0 += AT_KEYS) {
-    // stage: keys j0 .. j0 + 31 (zero past the sequence), the value tile transposed, the new table rows. The key
-    // tile reads distances q0 - j0 - 31 .. q0 - j0 + 63; the previous tile already loaded all but the lowest 32.
-    for (int id = tid; id < AT_KEYS * CH; id += 256) {
-      const int r = id / CH, c = (id % CH) * 8, key = j0 + r;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (key < len) {
-        kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ld + c);
-        vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * ld + c);
-      }
-      *reinterpret_cast<uint4*>(sK + r * S::DP + c) = kv;
-      const uint32_t va[4] = {vv.x, vv.y, vv.z, vv.w};
+  // a key tile's global data: keys j0 .. j0 + 31 (zero past the sequence), their values, and the 32 table rows of
+  // distances q0 - j0 - 31 .. q0 - j0 (the tile reads distances up to q0 - j0 + 63; the previous tiles brought
+  // those). Loaded into registers one tile ahead, so the loads of tile j0 + 32 fly while tile j0 computes.
+  constexpr int NC = (AT_KEYS * CH + 255) / 256;  // 16-byte chunks per thread and array
+  uint4 pk[NC], pv[NC], pr[NC];
+  auto fetch = [&](int j0) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        sVt[(c + 2 * k) * S::VT + r] = (uint16_t)(va[k] & 0xffff);
-        sVt[(c + 2 * k + 1) * S::VT + r] = (uint16_t)(va[k] >> 16);
+    for (int x = 0; x < NC; ++x) {
+      const int id = tid + x * 256;
+      pk[x] = pv[x] = pr[x] = make_uint4(0, 0, 0, 0);
+      if (id < AT_KEYS * CH) {
+        const int r = id / CH, c = (id % CH) * 8, key = j0 + r;
+        if (key < len) {
+          pk[x] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ld + c);
+          pv[x] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * ld + c);
+        }
+        const int d = q0 - j0 - (AT_KEYS - 1) + r, trow = min(max(d + p.rel_off, 0), p.rel_rows - 1);
+        pr[x] = *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
       }
     }
-    const int d_lo = q0 - j0 - (AT_KEYS - 1), d_hi = j0 == 0 ? q0 + AT_Q - 1 : d_lo + AT_KEYS - 1;
-    for (int id = tid; id < (d_hi - d_lo + 1) * CH; id += 256) {
-      const int d = d_lo + id / CH, c = (id % CH) * 8;
-      const int trow = min(max(d + p.rel_off, 0), p.rel_rows - 1), slot = (d + p.rel_off) & (AT_RING - 1);
-      *reinterpret_cast<uint4*>(sR + slot * S::DP + c) =
-          *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
+  };
+  auto stash = [&](int j0) {
+#pragma unroll
+    for (int x = 0; x < NC; ++x) {
+      const int id = tid + x * 256;
+      if (id < AT_KEYS * CH) {
+        const int r = id / CH, c = (id % CH) * 8;
+        *reinterpret_cast<uint4*>(sK + r * S::DP + c) = pk[x];
+        const uint32_t va[4] = {pv[x].x, pv[x].y, pv[x].z, pv[x].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          sVt[(c + 2 * k) * S::VT + r] = (uint16_t)(va[k] & 0xffff);
+          sVt[(c + 2 * k + 1) * S::VT + r] = (uint16_t)(va[k] >> 16);
+        }
+        const int d = q0 - j0 - (AT_KEYS - 1) + r;
+        *reinterpret_cast<uint4*>(sR + ((d + p.rel_off) & (AT_RING - 1)) * S::DP + c) = pr[x];
+      }
     }
+  };
+  // the first tile also reads distances q0 + 1 .. q0 + 63, straight into the ring
+  for (int id = tid; id < (AT_Q - 1) * CH; id += 256) {
+    const int d = q0 + 1 + id / CH, c = (id % CH) * 8;
+    const int trow = min(max(d + p.rel_off, 0), p.rel_rows - 1);
+    *reinterpret_cast<uint4*>(sR + ((d + p.rel_off) & (AT_RING - 1)) * S::DP + c) =
+        *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
+  }
+  fetch(0);
+  for (int j0 = 0; j0 < len; j0 += AT_KEYS) {
+    stash(j0);
     __syncthreads();
+    if (j0 + AT_KEYS < len) fetch(j0 + AT_KEYS);
 
     // content scores of keys kb * 16 + 4 g + e for this lane's query
     v4f s[2];
@@ -334,7 +362,9 @@ int dwconv_entry(const uint16_t* x, const float* w, const float* cb, const float
   const std::string nm(name);
   COHERE_REQUIRE(rows >= 0 && C > 0 && C % 8 == 0 && C <= 2048, nm + ": channels must be a multiple of 8, at most 2048");
   COHERE_REQUIRE(K == DW_K, nm + ": kernel size must be 9");
-  COHERE_REQUIRE(x && w && cb && bn_scale && bn_shift && seq_lo && seq_hi && al16(x), nm + ": bad pointer");
+  COHERE_REQUIRE(x && w && cb && bn_scale && bn_shift && seq_lo && seq_hi && al16(x) && al16(w) && al16(cb) &&
+                     al16(bn_scale) && al16(bn_shift),
+                 nm + ": bad pointer (x, the taps and the per-channel vectors 16-byte aligned)");
   COHERE_REQUIRE(Q8 ? (q && qs && (reinterpret_cast<uintptr_t>(q) & 7) == 0) : (y && al16(y)),
                  nm + ": bad output pointer");
   if (rows == 0) return 0;

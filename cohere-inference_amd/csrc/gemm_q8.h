@@ -90,7 +90,7 @@ struct Tile {
   static_assert(X_SLOTS % NW == 0 && W_SLOTS % NW == 0 && BN / NW <= 64, "DMA slots must split evenly over waves");
   static_assert(LPS * (ST - 1) <= 63 && ST >= 2 && ST <= 4, "vmcnt range");
   static_assert(SMEM <= LDS_BYTES, "LDS");
-  static_assert(BM * (BN / MS) * 4 <= PIPE, "SILU_Q8 row-max table reuses the pipeline buffers");
+  static_assert(BM * (BN / MS + BN / 64) * 4 <= PIPE, "SILU_Q8 row-max tables reuse the pipeline buffers");
   static_assert(!GROUPED || GMAX >= 1, "grouped tile needs room for scales");
 };
 
@@ -132,7 +132,9 @@ DEVI int sw128(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 // chunk `c` (0..3) of row `r` of a 64-byte-row tile
 DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
-template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE>
+// GS > 0 (grouped only): the K steps per scale group, fixed at compile time -- the main loop then runs whole groups
+// with the fold at a static place; GS == 0 reads it from p.group
+template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE, int GS = 0>
 __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) {
   using T = Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>;
   constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI, LPS = T::LPS;
@@ -165,7 +167,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   float* pW = pS + BM;
   float* pB = pW + BN;
   float* sS = pB + BN;
-  const int group_steps = GROUPED ? p.group / KSTEP : 1;
+  static_assert(GS == 0 || (GROUPED && GS % SPS == 0 && (GS % 2 == 0 || !T::PF)), "static group steps");
+  const int group_steps = GS > 0 ? GS : (GROUPED ? p.group / KSTEP : 1);
   const int G = GROUPED ? K / p.group : 1;
   const bool scales_in_lds = GROUPED && G <= T::GMAX;
   if constexpr (EPI != EPI_I32) {
@@ -238,20 +241,18 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   auto tok = [&](int i) { return wm * TM + i * MS + lrow; };
   auto chan = [&](int j, int q) { return wn * TN + j * MS + (MS == 16 ? lhi * 4 : 8 * q + 4 * lhi); };
 
-  // fold the finished K-group's int32 sums into fp32 with each token's scale of that group
-  auto fold = [&](int g) {
+  // grouped scales: at the first K step of each group, just before that step's matrix instruction for a block, the
+  // block's finished group sums are folded into fp32 with each token's scale of that group and reset. Interleaved
+  // with the next group's instructions, the fold reads results finished long before, so the matrix cores keep going.
+  auto group_scale = [&](int g, int i) {
+    const int r = tok(i);
+    return scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+  };
+  auto fold_block = [&](int j, int i, float sc) {
     if constexpr (GROUPED) {
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        const int r = tok(i);
-        const float sc = scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-#pragma unroll
-          for (int q = 0; q < RPL; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], sc, accf[j][i][q]);
-          acc[j][i] = Acc{};
-        }
-      }
+      for (int q = 0; q < RPL; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], sc, accf[j][i][q]);
+      acc[j][i] = Acc{};
     }
   };
 
@@ -294,24 +295,47 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     }
   };
   int kstep = 0;
-  auto mma = [&](const Frags& F) {
+  auto mma_block = [&](const Frags& F, int j, int i) {
+    if constexpr (SPARSE && MS == 16)
+      acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+    else if constexpr (SPARSE)
+      acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+    else if constexpr (MS == 16)
+      acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
+    else
+      acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
+  };
+  // one K step; with fold, the finished group gprev is folded block by block just before the block's instruction
+  auto mma_step = [&](const Frags& F, bool fold, int gprev) {
+    if (fold) {
+      float gsc[MI];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) gsc[i] = group_scale(gprev, i);
+#pragma unroll
+      for (int j = 0; j < NI; ++j)
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+          fold_block(j, i, gsc[i]);
+          mma_block(F, j, i);
+        }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
-      for (int i = 0; i < MI; ++i) {
-        if constexpr (SPARSE && MS == 16)
-          acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
-        else if constexpr (SPARSE)
-          acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
-        else if constexpr (MS == 16)
-          acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
-        else
-          acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
-      }
+      for (int i = 0; i < MI; ++i) mma_block(F, j, i);
+  };
+  auto mma = [&](const Frags& F) {
     if constexpr (GROUPED) {
+      const bool fold = kstep > 0 && kstep % group_steps == 0;  // uniform: this step also folds the last group
+      const int gprev = kstep / group_steps - 1;
       ++kstep;
-      if (kstep % group_steps == 0) fold(kstep / group_steps - 1);
+      if (fold) {
+        mma_step(F, true, gprev);
+        return;
+      }
     }
+    mma_step(F, false, 0);
   };
   // before reading step u, the first of stage t = u / SPS: stage t landed everywhere and stage t - 1 is free, so
   // stage t - 1 + ST can stream into its buffer
@@ -326,7 +350,31 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     if (s < KT) issue(s, s);
   wait_stages<LPS, ST>(min(KT - 1, ST - 1));
   lds_barrier();
-  if constexpr (T::PF) {
+  if constexpr (GS > 0) {
+    // whole groups of GS steps, unrolled: the fold sits at each group's first step (not the first group's), so the
+    // accumulators keep one register assignment through the loop
+    Frags F[T::PF ? 2 : 1];
+    if constexpr (T::PF) load_frags(F[0], 0);
+    auto group = [&](int g, auto fold_tag) {
+#pragma unroll
+      for (int s = 0; s < GS; ++s) {
+        const int u = g * GS + s;
+        if constexpr (T::PF) {
+          if (u + 1 < NSTEPS) {
+            if ((s + 1) % SPS == 0) enter_stage((u + 1) / SPS);
+            load_frags(F[(s + 1) & 1], u + 1);
+          }
+          mma_step(F[s & 1], decltype(fold_tag)::value && s == 0, g - 1);
+        } else {
+          if (u > 0 && s % SPS == 0) enter_stage(u / SPS);
+          load_frags(F[0], u);
+          mma_step(F[0], decltype(fold_tag)::value && s == 0, g - 1);
+        }
+      }
+    };
+    group(0, std::false_type{});
+    for (int g = 1; g < G; ++g) group(g, std::true_type{});
+  } else if constexpr (T::PF) {
     // fragments of step u + 1 are read while the matrix cores work on step u
     Frags F0, F1;
     load_frags(F0, 0);
@@ -351,6 +399,15 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       if (u > 0 && u % SPS == 0) enter_stage(u / SPS);
       load_frags(F0, u);
       mma(F0);
+    }
+  }
+
+  if constexpr (GROUPED) {  // the last group
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+      const float sc = group_scale(G - 1, i);
+#pragma unroll
+      for (int j = 0; j < NI; ++j) fold_block(j, i, sc);
     }
   }
 
@@ -451,15 +508,30 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
           if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
         }
       __syncthreads();
-      const int blocks = p.qgroup / MS;
+      // each (row, column group) maximum once, from the block table, into gmax [BM][BN / qgroup]
+      const int blocks = p.qgroup / MS, ngroups = BN / p.qgroup;
+      float* gmax = red + BM * CB;
+      for (int id = tid; id < BM * ngroups; id += NT) {
+        const float* src = red + (id / ngroups) * CB + (id % ngroups) * blocks;
+        float mx = 0.f;
+        if (blocks % 4 == 0) {
+          for (int b = 0; b < blocks; b += 4) {
+            const v4f v = *reinterpret_cast<const v4f*>(src + b);
+            mx = fmaxf(mx, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
+          }
+        } else {
+          for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, src[b]);
+        }
+        gmax[id] = mx;
+      }
+      __syncthreads();
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int rl = tok(i), m = m0 + rl;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
           const int cb = (wn * TN + j * MS) / MS, g0 = cb - cb % blocks;
-          float mx = 0.f;
-          for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, red[rl * CB + g0 + b]);
+          const float mx = gmax[rl * ngroups + cb / blocks];
           const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
           if (m >= M) continue;
 #pragma unroll
@@ -483,6 +555,15 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE>
 void launch_tile(const GemmArgs& p, hipStream_t s) {
   const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
+  // the feed-forward W2's grouping (256 K per scale) runs the static-group loop (tiles of one wave per SIMD: with
+  // two, its unrolled groups do not fit the registers)
+  constexpr int GS = 256 / Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::KSTEP;
+  if constexpr (GROUPED && EPI == EPI_RESID && WM * WN <= 4) {
+    if (p.group == 256) {
+      gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE, GS><<<grid, WM * WN * 64, 0, s>>>(p);
+      return;
+    }
+  }
   gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
 }
 
