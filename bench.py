@@ -19,7 +19,8 @@ the same workload (dense on the pruned weights, as the CPU has no 2:4 path), nex
 Extras (not the metric): config 0 (dense W8A8 5120x1280, bias) TOPS against the dense peak; config 3's decoder-
 step projections (M=64, 8 layers + head, all int8 weights) in GB/s against 8 TB/s, cold-cache (weight sets rotated so
 the 256 MB Infinity Cache cannot hold them); config 2's FastConformer block through the native layer loop (ms per
-block, its GEMM TOPS, and the audio-sec/sec 24 such blocks would give).
+block, its GEMM TOPS, and the audio-sec/sec 24 such blocks would give); config 3's captured decoder step (64 slots, ms
+per step, tokens/s, weights + KV bytes per second against 8 TB/s).
 """
 
 from __future__ import annotations
@@ -47,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block"], default=None,
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block", "decstep"], default=None,
                     help="run one part only (for rocprofv3 runs)")
     ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
     return ap.parse_args()
@@ -286,6 +287,85 @@ def block_extra(dev, replays=20):
                     "front end, subsampling or decoder"}
 
 
+def random_decoder(seed: int, dev):
+    """Config 3's decoder: transformers CohereAsrDecoder (8 layers, d 1024, 8 heads of 128, FFN 4096, vocab 16384)
+    + output head, seeded N(0, 0.05) weights and biases, LayerNorm affines around (1, 0), bf16 on the GPU; `proj` the
+    identity (the cross-attention memory is drawn at decoder width)."""
+    import types
+
+    import torch
+    from transformers.models.cohere_asr.configuration_cohere_asr import CohereAsrConfig
+    from transformers.models.cohere_asr.modeling_cohere_asr import CohereAsrDecoder
+
+    cfg = CohereAsrConfig(encoder_config={"model_type": "parakeet_encoder", "hidden_size": 1024})
+    torch.manual_seed(seed)
+    dec = CohereAsrDecoder(cfg).eval()
+    head = torch.nn.Linear(cfg.hidden_size, cfg.vocab_size)
+    g = torch.Generator().manual_seed(seed + 1)
+    with torch.no_grad():
+        for mod in (dec, head):
+            for name, p in mod.named_parameters():
+                if name.startswith("proj."):
+                    continue
+                base = (1.0 if name.endswith("weight") else 0.0) if "norm" in name else 0.0
+                p.copy_(base + (0.1 if "norm" in name else 0.05) * torch.randn(p.shape, generator=g))
+        dec.proj.weight.copy_(torch.eye(cfg.hidden_size))
+        dec.proj.bias.zero_()
+    return types.SimpleNamespace(model=types.SimpleNamespace(decoder=dec.to(dev, torch.bfloat16)),
+                                 proj_out=head.to(dev, torch.bfloat16), config=cfg)
+
+
+def decoder_step_extra(dev, steps=448):
+    """Config 3: B=64 active slots, self-attention caches of U(1..448) positions (seeded), cross-attention over 375
+    frames of N(0,1) memory per slot; the captured step (bucket 64, int8 qkv/fc1/fc2/head, bf16 o/cq/co, int8 KV
+    caches -- the reference's int8 layout) replayed `steps` times."""
+    import torch
+
+    from kernels.stream_decoder import StreamDecoder
+
+    model = random_decoder(3, dev)
+    B, F_ = 64, 375
+    dec = StreamDecoder(model, slots=B, max_new_tokens=448, max_prompt=16, buckets=(64,), int8=True, frames=F_)
+    g = torch.Generator().manual_seed(4)
+    mem = torch.randn(B * F_, 1024, generator=g).to(torch.bfloat16).to(dev)
+    slots = list(range(B))
+    dec.fill_cross(mem, [F_] * B, slots, projected=True)
+    dec.admit(slots, [torch.tensor([4])] * B, [F_] * B)
+    lens = torch.randint(1, 449, (B,), generator=g)
+    with torch.cuda.stream(dec.stream):
+        dec.pos[:B] = lens.to(torch.int32).to(dev)
+        dec.self_k.copy_(torch.randint(-127, 128, dec.self_k.shape, dtype=torch.int8, device=dev))
+        dec.self_v.copy_(torch.randint(-127, 128, dec.self_v.shape, dtype=torch.int8, device=dev))
+        dec.self_ks.fill_(0.01)
+        dec.self_vs.fill_(0.01)
+    b = dec.set_active(slots)
+    dec.stream.synchronize()
+    for _ in range(3):
+        dec.step(b)
+    dec.stream.synchronize()
+    len0 = float(dec.pos[:B].float().mean())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(dec.stream):
+        e0.record()
+        for _ in range(steps):
+            dec.graphs[b].replay()
+        e1.record()
+    dec.stream.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    weights = sum(t.numel() * t.element_size() for ly in dec.layers
+                  for t in (ly.qkv_w8[0], ly.fc1_w8[0], ly.fc2_w8[0], ly.o[0], ly.cq[0], ly.co[0]))
+    weights += dec.head_w8[0].numel()
+    mean_len = (len0 + float(dec.pos[:B].float().mean())) / 2  # over the timed steps
+    kv = 8 * B * 2 * 1024 * (mean_len + F_)  # int8 keys + values read per step (8 layers), scales aside
+    return {"what": "config 3: one captured decoder step, 64 active slots, self-KV lengths U(1..448), cross-attention "
+                    "over 375 frames, int8 qkv/fc1/fc2/head + bf16 o/cq/co (the reference's int8 layout), int8 KV "
+                    f"caches; replayed {steps} times",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B / (ms * 1e-3), 1),
+            "weight_bytes": weights, "kv_bytes_mean": int(kv),
+            "GBps_weights_plus_kv": round((weights + kv) / (ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm": round((weights + kv) / (ms * 1e-3) / PEAK_HBM, 4)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -383,6 +463,8 @@ def main():
 
     if not args.no_extras and args.only in (None, "block"):
         result["encoder_block"] = block_extra(dev)
+    if not args.no_extras and args.only in (None, "decstep"):
+        result["decoder_step"] = decoder_step_extra(dev)
 
     if args.only is not None:
         print(json.dumps(result))
@@ -403,7 +485,7 @@ def main():
         "kernels_ms": result["kernels_ms"],
     }
     line["frac_of_sparse_peak"] = round(line["value"] * 1e12 / PEAK_INT8_SPARSE, 4)
-    for k in ("dense_config0", "decoder_gemms", "encoder_block"):
+    for k in ("dense_config0", "decoder_gemms", "encoder_block", "decoder_step"):
         if k in result:
             line[k] = result[k]
     if not args.no_cpu:

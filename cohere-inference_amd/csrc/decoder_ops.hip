@@ -1,0 +1,511 @@
+// One decoding step's non-GEMM kernels for continuous batching (reference kernels/csrc/decoder_ops.cu,
+// kernels/csrc/dec_attn.cuh), for gfx950. Row r of a step works on slot active[r] of the per-slot state and caches,
+// so rows join and leave between steps without moving any cache.
+//
+//   dec_embed       x = LN0(bf16(embed[token] + pos_table[position])), h = LN1(x)           (decoder_ops.cu:24-54)
+//   dec_add_ln      x = bf16(x + y), h = LN(x)                                                  (decoder_ops.cu:56-83)
+//   dec_attention   softmax(q k^T scale) v of one new token per row over its slot's cache; self-attention first
+//                   writes the new key and value at position pos (int8 caches: quantized with one scale per
+//                   128-vector) and attends to it unquantized; cross-attention reads the slot's audio frames
+//                                                                                               (dec_attn.cuh:84-188)
+//   dec_pick        greedy choice (first index of the maximum), the forced prompt, pad once finished, end at the
+//                   end-of-text token or the slot's limit; advances the position                (decoder_ops.cu:106-159)
+//   dec_scatter_kv  cross-attention keys/values of packed encoder frames into their slots (bf16, or int8 with a
+//                   scale per 128-vector)                                                       (decoder_ops.cu:163-204)
+#include "cohere_hip.h"
+#include "common.h"
+#include "rows.h"
+
+#include <string>
+
+namespace {
+
+using namespace cohere_rows;
+
+constexpr int HD = 128;  // head size
+
+// ---- embedding and residual LayerNorms: one wave per row ------------------------------------------------------------
+
+template <int VEC>
+__global__ void __launch_bounds__(256) dec_embed_kernel(const int32_t* __restrict__ active,
+                                                        const int64_t* __restrict__ tok, const int32_t* __restrict__ pos,
+                                                        const uint16_t* __restrict__ emb, const uint16_t* __restrict__ ptab,
+                                                        const uint16_t* w0, const uint16_t* b0, float eps0,
+                                                        const uint16_t* w1, const uint16_t* b1, float eps1, uint16_t* x,
+                                                        uint16_t* h, int rows, int width) {
+  const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
+  if (row >= rows) return;
+  const int s = active[row];
+  const int64_t t = tok[s];
+  const int p = pos[s];
+  Row<VEC> e, q;
+  load_row<VEC>(emb + t * width, width, lane, e);
+  load_row<VEC>(ptab + (int64_t)p * width, width, lane, q);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) e.v[i][k] = round_bf(e.v[i][k] + q.v[i][k]);
+  ln_row<VEC>(e, width, lane, w0, b0, eps0);
+  store_row<VEC>(e, width, lane, x + (int64_t)row * width);
+  ln_row<VEC>(e, width, lane, w1, b1, eps1);
+  store_row<VEC>(e, width, lane, h + (int64_t)row * width);
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ y,
+                                                         int64_t ldy, const uint16_t* w, const uint16_t* b, float eps,
+                                                         uint16_t* h, int rows, int width) {
+  const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
+  if (row >= rows) return;
+  Row<VEC> a, d;
+  load_row<VEC>(x + (int64_t)row * width, width, lane, a);
+  load_row<VEC>(y + (int64_t)row * ldy, width, lane, d);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a.v[i][k] = round_bf(a.v[i][k] + d.v[i][k]);
+  store_row<VEC>(a, width, lane, x + (int64_t)row * width);
+  ln_row<VEC>(a, width, lane, w, b, eps);
+  store_row<VEC>(a, width, lane, h + (int64_t)row * width);
+}
+
+// ---- attention of one new token per row ---------------------------------------------------------------------------
+// A workgroup of 256 threads per (row, head, split): 32 groups of 8 lanes, each lane 16 of the 128 dims, each group
+// streaming every 32nd key of the split (two in flight). Per key: the group's partial dot products meet through
+// three lane shuffles; the online softmax runs in fp32 per group; the 32 groups are combined through LDS at the end
+// (or, with several splits, written as partials (o[128], max, sum) for dec_combine).
+struct DecAttnArgs {
+  const int32_t* active;
+  const uint16_t* q;  // (rows, ldq): head h at column h * 128 (self: q | k | v of the new token)
+  int64_t ldq;
+  uint16_t* k;        // bf16 caches (slots, H, T, 128)
+  uint16_t* v;
+  int8_t* k8;         // int8 caches (slots, H, T, 128) with scales (slots, H, T)
+  int8_t* v8;
+  float* ks;
+  float* vs;
+  const int32_t* n;   // self: position of the new token per slot; cross: audio frames per slot
+  int H, T;
+  float scale;
+  uint16_t* out;      // (rows, H * 128)
+  float* part;        // (rows, H, splits, 130) when split
+};
+
+constexpr int AG = 32;  // key groups per workgroup
+
+DEVI void load16_bf(const uint16_t* p, float (&f)[16]) {
+  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+}
+
+DEVI void load16_q8(const int8_t* p, float s, float (&f)[16]) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) f[k] = (float)(int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xff) * s;
+}
+
+// group-of-8 reductions (lanes 8g .. 8g+7 of a wave)
+DEVI float group_sum(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  return v;
+}
+DEVI float group_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 1, 64));
+  v = fmaxf(v, __shfl_xor(v, 2, 64));
+  v = fmaxf(v, __shfl_xor(v, 4, 64));
+  return v;
+}
+
+// the 16 values a lane holds of a 128-vector as int8 with the vector's scale (absmax / 127 over the 8 lanes)
+DEVI void store16_q8(const float (&f)[16], int8_t* dst, float* scale, int gl) {
+  float mx = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) mx = fmaxf(mx, fabsf(f[k]));
+  mx = group_max(mx);
+  const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+  uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int q = (int)rintf(fminf(fmaxf(f[k] * inv, -127.f), 127.f));
+    w[k >> 2] |= (uint32_t)(q & 0xff) << ((k & 3) * 8);
+  }
+  *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  if (gl == 0) *scale = sc;
+}
+
+DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&vv)[16], float scale, float& m,
+                     float& l, float (&acc)[16]) {
+  float d = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) d = __builtin_fmaf(q[k], kk[k], d);
+  d = group_sum(d);
+  const float s = d * scale, mn = fmaxf(m, s), a = __expf(m - mn), e = __expf(s - mn);
+  l = __builtin_fmaf(l, a, e);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(acc[k], a, e * vv[k]);
+  m = mn;
+}
+
+template <bool SELF, bool Q8>
+__global__ void __launch_bounds__(256) dec_attention_kernel(const DecAttnArgs p) {
+  __shared__ float sm[AG], sl[AG];
+  __shared__ float sacc[AG][HD + 4];
+  const int r = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
+  const int s = p.active[r];
+  const int tid = threadIdx.x, grp = tid >> 3, gl = tid & 7;
+  float q[16];
+  load16_bf(p.q + (int64_t)r * p.ldq + h * HD + gl * 16, q);
+  const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
+  const int n = p.n[s];
+  float m = -INFINITY, l = 0.f, acc[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+  if (SELF && sp == 0 && grp == 0) {  // the new key and value: into the cache at n, and attended as computed
+    float kn[16], vn[16];
+    const uint16_t* row = p.q + (int64_t)r * p.ldq + p.H * HD + h * HD + gl * 16;
+    load16_bf(row, kn);
+    load16_bf(row + p.H * HD, vn);
+    const int64_t vec = vec0 + n;
+    if constexpr (Q8) {
+      store16_q8(kn, p.k8 + vec * HD + gl * 16, p.ks + vec, gl);
+      store16_q8(vn, p.v8 + vec * HD + gl * 16, p.vs + vec, gl);
+    } else {
+      uint16_t* kd = p.k + vec * HD + gl * 16;
+      uint16_t* vd = p.v + vec * HD + gl * 16;
+      *reinterpret_cast<uint4*>(kd) = *reinterpret_cast<const uint4*>(row);
+      *reinterpret_cast<uint4*>(kd + 8) = *reinterpret_cast<const uint4*>(row + 8);
+      *reinterpret_cast<uint4*>(vd) = *reinterpret_cast<const uint4*>(row + p.H * HD);
+      *reinterpret_cast<uint4*>(vd + 8) = *reinterpret_cast<const uint4*>(row + p.H * HD + 8);
+    }
+    attend_one(q, kn, vn, p.scale, m, l, acc);
+  }
+  const int chunk = (n + nsp - 1) / nsp, start = sp * chunk, end = min(n, start + chunk);
+  int j = start + grp;
+  auto key = [&](int jj, float (&kk)[16], float (&vv)[16]) {
+    const int64_t vec = vec0 + jj;
+    if constexpr (Q8) {
+      load16_q8(p.k8 + vec * HD + gl * 16, p.ks[vec], kk);
+      load16_q8(p.v8 + vec * HD + gl * 16, p.vs[vec], vv);
+    } else {
+      load16_bf(p.k + vec * HD + gl * 16, kk);
+      load16_bf(p.v + vec * HD + gl * 16, vv);
+    }
+  };
+  for (; j + AG < end; j += 2 * AG) {
+    float k0[16], v0[16], k1[16], v1[16];
+    key(j, k0, v0);
+    key(j + AG, k1, v1);
+    attend_one(q, k0, v0, p.scale, m, l, acc);
+    attend_one(q, k1, v1, p.scale, m, l, acc);
+  }
+  if (j < end) {
+    float k0[16], v0[16];
+    key(j, k0, v0);
+    attend_one(q, k0, v0, p.scale, m, l, acc);
+  }
+  // combine the groups: weights exp(m_g - M)
+  if (gl == 0) {
+    sm[grp] = m;
+    sl[grp] = l;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sacc[grp][gl * 16 + k] = acc[k];
+  __syncthreads();
+  if (tid >= HD) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < AG; ++g) M = fmaxf(M, sm[g]);
+  float L = 0.f, O = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll 8
+    for (int g = 0; g < AG; ++g) {
+      const float w = __expf(sm[g] - M);
+      L = __builtin_fmaf(w, sl[g], L);
+      O = __builtin_fmaf(w, sacc[g][tid], O);
+    }
+  }
+  if (nsp == 1) {
+    p.out[(int64_t)r * p.H * HD + h * HD + tid] = f2bf(O / L);
+  } else {
+    float* part = p.part + (((int64_t)r * p.H + h) * nsp + sp) * (HD + 2);
+    part[tid] = O;
+    if (tid == 0) {
+      part[HD] = M;
+      part[HD + 1] = L;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(HD) dec_combine_kernel(const float* __restrict__ part, int nsp, uint16_t* out,
+                                                         int H) {
+  const int r = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const float* base = part + ((int64_t)r * H + h) * nsp * (HD + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < nsp; ++s) M = fmaxf(M, base[s * (HD + 2) + HD]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < nsp; ++s) {
+    const float* q = base + s * (HD + 2);
+    const float w = q[HD] == -INFINITY ? 0.f : __expf(q[HD] - M);
+    L = __builtin_fmaf(w, q[HD + 1], L);
+    O = __builtin_fmaf(w, q[d], O);
+  }
+  out[(int64_t)r * H * HD + h * HD + d] = f2bf(O / L);
+}
+
+// ---- greedy choice -------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restrict__ logits, int V,
+                                                       const int32_t* __restrict__ active, int dummy, int64_t* tok,
+                                                       int32_t* pos, uint8_t* finished, const int64_t* forced, int FP,
+                                                       const int32_t* plen, const int32_t* limit, int64_t* out, int OUT,
+                                                       int64_t pad, int64_t eos) {
+  __shared__ float sb[4];
+  __shared__ int sa[4];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const int s = active[r];
+  if (s == dummy) return;
+  const uint16_t* row = logits + (int64_t)r * V;
+  float best = -INFINITY;
+  int arg = 0x7fffffff;
+  for (int i = tid * 8; i < V; i += 256 * 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(row + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v = __uint_as_float(k & 1 ? w[k >> 1] & 0xffff0000u : w[k >> 1] << 16);
+      if (v > best) {  // strictly greater: the first index of a tie stays
+        best = v;
+        arg = i + k;
+      }
+    }
+  }
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ob = __shfl_xor(best, o, 64);
+    const int oa = __shfl_xor(arg, o, 64);
+    if (ob > best || (ob == best && oa < arg)) {
+      best = ob;
+      arg = oa;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sb[tid >> 6] = best;
+    sa[tid >> 6] = arg;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w = 1; w < 4; ++w)
+    if (sb[w] > best || (sb[w] == best && sa[w] < arg)) {
+      best = sb[w];
+      arg = sa[w];
+    }
+  if (finished[s]) return;  // ended at an earlier step: nothing moves until the host retires the slot
+  const int at = pos[s] + 1;
+  const bool in_prompt = at < plen[s];
+  const int64_t nt = in_prompt ? forced[(int64_t)s * FP + at] : (int64_t)arg;
+  out[(int64_t)s * OUT + at] = nt;
+  tok[s] = nt;
+  pos[s] = at;
+  finished[s] = (!in_prompt && (nt == eos || at >= limit[s])) ? 1 : 0;
+  (void)pad;
+}
+
+// ---- cross-attention keys and values into their slots --------------------------------------------------------------
+// kv (rows, L * 2 * H * 128) of packed frames (per layer: k heads then v heads), row i = frame frame_of[i] of slot
+// slot_of[i]; caches (L, S, H, T, 128). 16 threads per 128-vector.
+template <bool Q8>
+__global__ void __launch_bounds__(256) dec_scatter_kv_kernel(const uint16_t* __restrict__ kv,
+                                                             const int32_t* __restrict__ slot_of,
+                                                             const int32_t* __restrict__ frame_of, uint16_t* ck,
+                                                             uint16_t* cv, int8_t* ck8, int8_t* cv8, float* cks,
+                                                             float* cvs, int rows, int L, int S, int H, int T) {
+  const int chunks = L * 2 * H * (HD / 8);
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // rows * chunks is a multiple of 16
+  const bool live = idx < (int64_t)rows * chunks;
+  const int row = live ? (int)(idx / chunks) : 0, c = live ? (int)(idx % chunks) : 0;
+  const int d8 = c % (HD / 8), h = (c / (HD / 8)) % H, kvi = (c / (HD / 8 * H)) % 2, l = c / (HD / 8 * H * 2);
+  uint4 u = make_uint4(0, 0, 0, 0);
+  if (live) u = *reinterpret_cast<const uint4*>(kv + (int64_t)row * chunks * 8 + (int64_t)c * 8);
+  const int64_t vec = live ? ((((int64_t)l * S + slot_of[row]) * H + h) * T + frame_of[row]) : 0;
+  if constexpr (!Q8) {
+    if (live) *reinterpret_cast<uint4*>((kvi ? cv : ck) + vec * HD + d8 * 8) = u;
+  } else {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float f[8], mx = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      f[k] = __uint_as_float(k & 1 ? w[k >> 1] & 0xffff0000u : w[k >> 1] << 16);
+      mx = fmaxf(mx, fabsf(f[k]));
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    if (!live) return;
+    const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+    uint32_t q[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int qi = (int)rintf(fminf(fmaxf(f[k] * inv, -127.f), 127.f));
+      q[k >> 2] |= (uint32_t)(qi & 0xff) << ((k & 3) * 8);
+    }
+    *reinterpret_cast<uint2*>((kvi ? cv8 : ck8) + vec * HD + d8 * 8) = make_uint2(q[0], q[1]);
+    if (d8 == 0) (kvi ? cvs : cks)[vec] = sc;
+  }
+}
+
+bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
+
+int vec_of(int64_t width) { return (int)((width + 511) / 512); }
+
+}  // namespace
+
+extern "C" int cohere_dec_embed(const int32_t* active, int64_t rows, const int64_t* tok, const int32_t* pos,
+                                const uint16_t* emb, const uint16_t* ptab, const uint16_t* w0, const uint16_t* b0,
+                                float eps0, const uint16_t* w1, const uint16_t* b1, float eps1, uint16_t* x,
+                                uint16_t* h, int64_t width, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && width > 0 && width % 8 == 0 && width <= 2048,
+                 "dec_embed: width must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(active && tok && pos && emb && ptab && w0 && b0 && w1 && b1 && x && h && al16(emb) && al16(ptab) &&
+                     al16(x) && al16(h) && al16(w0) && al16(b0) && al16(w1) && al16(b1),
+                 "dec_embed: bad pointer");
+  if (rows == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int grid = (int)((rows + 3) / 4);
+#define EMB(V)                                                                                                      \
+  dec_embed_kernel<V><<<grid, 256, 0, st>>>(active, tok, pos, emb, ptab, w0, b0, eps0, w1, b1, eps1, x, h, (int)rows, \
+                                            (int)width)
+  switch (vec_of(width)) {
+    case 1: EMB(1); break;
+    case 2: EMB(2); break;
+    case 3: EMB(3); break;
+    default: EMB(4); break;
+  }
+#undef EMB
+  return cohere::check_launch("dec_embed");
+}
+
+extern "C" int cohere_dec_add_ln(uint16_t* x, const uint16_t* y, int64_t ldy, const uint16_t* w, const uint16_t* b,
+                                 float eps, uint16_t* h, int64_t rows, int64_t width, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && width > 0 && width % 8 == 0 && width <= 2048,
+                 "dec_add_ln: width must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(x && y && w && b && h && al16(x) && al16(y) && ldy % 8 == 0 && al16(w) && al16(b) && al16(h),
+                 "dec_add_ln: bad pointer");
+  if (rows == 0) return 0;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int grid = (int)((rows + 3) / 4);
+#define ADD(V) dec_add_ln_kernel<V><<<grid, 256, 0, st>>>(x, y, ldy, w, b, eps, h, (int)rows, (int)width)
+  switch (vec_of(width)) {
+    case 1: ADD(1); break;
+    case 2: ADD(2); break;
+    case 3: ADD(3); break;
+    default: ADD(4); break;
+  }
+#undef ADD
+  return cohere::check_launch("dec_add_ln");
+}
+
+namespace {
+int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t splits, int64_t part_len,
+                    void* stream, const char* name) {
+  const std::string nm(name);
+  COHERE_REQUIRE(rows >= 0 && p.H > 0 && p.H <= 65535 && p.T > 0 && splits >= 1 && splits <= 64, nm + ": bad sizes");
+  COHERE_REQUIRE(p.active && p.q && p.n && p.out && al16(p.q) && p.ldq % 8 == 0 && al16(p.out),
+                 nm + ": bad pointer");
+  COHERE_REQUIRE(q8 ? (p.k8 && p.v8 && p.ks && p.vs && al16(p.k8) && al16(p.v8)) : (p.k && p.v && al16(p.k) && al16(p.v)),
+                 nm + ": bad cache pointer");
+  COHERE_REQUIRE(splits == 1 || (p.part && part_len >= rows * p.H * splits * (HD + 2)),
+                 nm + ": splits > 1 needs part with rows x H x splits x 130 floats");
+  if (rows == 0) return 0;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)rows, (unsigned)p.H, (unsigned)splits);
+  if (self) {
+    if (q8) dec_attention_kernel<true, true><<<grid, 256, 0, s>>>(p);
+    else dec_attention_kernel<true, false><<<grid, 256, 0, s>>>(p);
+  } else {
+    if (q8) dec_attention_kernel<false, true><<<grid, 256, 0, s>>>(p);
+    else dec_attention_kernel<false, false><<<grid, 256, 0, s>>>(p);
+  }
+  if (splits > 1) dec_combine_kernel<<<dim3((unsigned)rows, (unsigned)p.H), HD, 0, s>>>(p.part, (int)splits, p.out, p.H);
+  return cohere::check_launch(name);
+}
+}  // namespace
+
+extern "C" int cohere_dec_attention(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
+                                    uint16_t* k, uint16_t* v, const int32_t* n, int64_t heads, int64_t T, float scale,
+                                    int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream) {
+  cohere::clear_error();
+  DecAttnArgs p{};
+  p.active = active; p.q = q; p.ldq = ldq; p.k = k; p.v = v; p.n = n; p.H = (int)heads; p.T = (int)T;
+  p.scale = scale; p.out = out; p.part = part;
+  return attention_entry(self != 0, false, p, rows, splits, part_len, stream, "dec_attention");
+}
+
+extern "C" int cohere_dec_attention_q8(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q,
+                                       int64_t ldq, int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n,
+                                       int64_t heads, int64_t T, float scale, int64_t splits, float* part,
+                                       int64_t part_len, uint16_t* out, void* stream) {
+  cohere::clear_error();
+  DecAttnArgs p{};
+  p.active = active; p.q = q; p.ldq = ldq; p.k8 = k8; p.v8 = v8; p.ks = ks; p.vs = vs; p.n = n; p.H = (int)heads;
+  p.T = (int)T; p.scale = scale; p.out = out; p.part = part;
+  return attention_entry(self != 0, true, p, rows, splits, part_len, stream, "dec_attention_q8");
+}
+
+extern "C" int cohere_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active, int64_t dummy,
+                               int64_t* tok, int32_t* pos, uint8_t* finished, const int64_t* forced, int64_t FP,
+                               const int32_t* plen, const int32_t* limit, int64_t* out, int64_t OUT, int64_t pad,
+                               int64_t eos, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && V > 0 && V % 8 == 0, "dec_pick: the vocabulary must be a multiple of 8");
+  COHERE_REQUIRE(logits && active && tok && pos && finished && forced && plen && limit && out && al16(logits),
+                 "dec_pick: bad pointer");
+  if (rows == 0) return 0;
+  dec_pick_kernel<<<(unsigned)rows, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      logits, (int)V, active, (int)dummy, tok, pos, finished, forced, (int)FP, plen, limit, out, (int)OUT, pad, eos);
+  return cohere::check_launch("dec_pick");
+}
+
+namespace {
+int scatter_entry(bool q8, const uint16_t* kv, int64_t rows, const int32_t* slot_of, const int32_t* frame_of,
+                  uint16_t* ck, uint16_t* cv, int8_t* ck8, int8_t* cv8, float* cks, float* cvs, int64_t L, int64_t S,
+                  int64_t H, int64_t T, void* stream, const char* name) {
+  const std::string nm(name);
+  COHERE_REQUIRE(rows >= 0 && L > 0 && S > 0 && H > 0 && T > 0, nm + ": bad sizes");
+  COHERE_REQUIRE(kv && slot_of && frame_of && al16(kv), nm + ": bad pointer");
+  COHERE_REQUIRE(q8 ? (ck8 && cv8 && cks && cvs) : (ck && cv && al16(ck) && al16(cv)), nm + ": bad cache pointer");
+  if (rows == 0) return 0;
+  const int64_t n = rows * L * 2 * H * (HD / 8);
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (q8)
+    dec_scatter_kv_kernel<true><<<grid, 256, 0, s>>>(kv, slot_of, frame_of, nullptr, nullptr, ck8, cv8, cks, cvs,
+                                                     (int)rows, (int)L, (int)S, (int)H, (int)T);
+  else
+    dec_scatter_kv_kernel<false><<<grid, 256, 0, s>>>(kv, slot_of, frame_of, ck, cv, nullptr, nullptr, nullptr,
+                                                      nullptr, (int)rows, (int)L, (int)S, (int)H, (int)T);
+  return cohere::check_launch(name);
+}
+}  // namespace
+
+extern "C" int cohere_dec_scatter_kv(const uint16_t* kv, int64_t rows, const int32_t* slot_of, const int32_t* frame_of,
+                                     uint16_t* ck, uint16_t* cv, int64_t L, int64_t S, int64_t H, int64_t T,
+                                     void* stream) {
+  cohere::clear_error();
+  return scatter_entry(false, kv, rows, slot_of, frame_of, ck, cv, nullptr, nullptr, nullptr, nullptr, L, S, H, T,
+                       stream, "dec_scatter_kv");
+}
+
+extern "C" int cohere_dec_scatter_kv_q8(const uint16_t* kv, int64_t rows, const int32_t* slot_of,
+                                        const int32_t* frame_of, int8_t* ck, int8_t* cv, float* cks, float* cvs,
+                                        int64_t L, int64_t S, int64_t H, int64_t T, void* stream) {
+  cohere::clear_error();
+  return scatter_entry(true, kv, rows, slot_of, frame_of, nullptr, nullptr, ck, cv, cks, cvs, L, S, H, T, stream,
+                       "dec_scatter_kv_q8");
+}

@@ -5,58 +5,15 @@
 // One wave per row; each lane holds up to VEC 8-element chunks of the row in registers (16-byte loads), so a row is
 // read once and written once. The quantization arithmetic is the reference's: mx = max|bf16 x|, s = mx > 0 ?
 // mx / 127 : 1, inv = 1 / s (both correctly rounded fp32 divisions), q = rint_half_even(clamp(x * inv, +-127)).
-#include "common.h"
 #include "cohere_hip.h"
+#include "common.h"
+#include "rows.h"
 
 #include <string>
 
 namespace {
 
-template <int VEC>
-struct Row {
-  float v[VEC][8];
-};
-
-template <int VEC>
-DEVI void load_row(const uint16_t* x, int cols, int lane, Row<VEC>& r) {
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    uint4 u = make_uint4(0, 0, 0, 0);
-    if (c < cols) u = *reinterpret_cast<const uint4*>(x + c);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      r.v[i][2 * k] = __uint_as_float(w[k] << 16);
-      r.v[i][2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-    }
-  }
-}
-
-// the row (already bf16 values) as int8 with one scale per row
-template <int VEC>
-DEVI void store_q8(const Row<VEC>& r, int cols, int lane, int8_t* q, float* scale) {
-  float mx = 0.f;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(r.v[i][k]));
-  mx = wave_max_xor(mx, 64);
-  const float s = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / s;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    if (c >= cols) continue;
-    uint32_t w[2] = {0, 0};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int v = (int)rintf(fminf(fmaxf(r.v[i][k] * inv, -127.f), 127.f));
-      w[k >> 2] |= (uint32_t)(v & 0xff) << ((k & 3) * 8);
-    }
-    *reinterpret_cast<uint2*>(q + c) = make_uint2(w[0], w[1]);
-  }
-  if (lane == 0) *scale = s;
-}
+using namespace cohere_rows;
 
 template <int VEC>
 __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx,
@@ -67,61 +24,6 @@ __global__ void __launch_bounds__(256) quantize_rows_kernel(const uint16_t* __re
   Row<VEC> r;
   load_row<VEC>(x + (int64_t)row * ldx, cols, lane, r);
   store_q8<VEC>(r, cols, lane, q + (int64_t)row * ldq, s + row);
-}
-
-DEVI float wave_sum(float v) {
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-// LayerNorm of the row in place (fp32 statistics over the bf16 inputs), the result rounded to bf16
-template <int VEC>
-DEVI void ln_row(Row<VEC>& r, int cols, int lane, const uint16_t* w, const uint16_t* b, float eps) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) s += r.v[i][k];
-  const float mean = wave_sum(s) / (float)cols;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    if ((i * 64 + lane) * 8 >= cols) continue;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float d = r.v[i][k] - mean;
-      q += d * d;
-    }
-  }
-  const float rstd = 1.f / sqrtf(wave_sum(q) / (float)cols + eps);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    if (c >= cols) continue;
-    const uint4 wv = *reinterpret_cast<const uint4*>(w + c), bv = *reinterpret_cast<const uint4*>(b + c);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, bb[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float wk = __uint_as_float(k & 1 ? ww[k >> 1] & 0xffff0000u : ww[k >> 1] << 16);
-      const float bk = __uint_as_float(k & 1 ? bb[k >> 1] & 0xffff0000u : bb[k >> 1] << 16);
-      r.v[i][k] = round_bf(__builtin_fmaf((r.v[i][k] - mean) * rstd, wk, bk));
-    }
-  }
-}
-
-template <int VEC>
-DEVI void store_row(const Row<VEC>& r, int cols, int lane, uint16_t* x) {
-#pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    if (c >= cols) continue;
-    uint4 u;
-    u.x = pack_bf2(r.v[i][0], r.v[i][1]);
-    u.y = pack_bf2(r.v[i][2], r.v[i][3]);
-    u.z = pack_bf2(r.v[i][4], r.v[i][5]);
-    u.w = pack_bf2(r.v[i][6], r.v[i][7]);
-    *reinterpret_cast<uint4*>(x + c) = u;
-  }
 }
 
 // h = LN(x); with TWO, x = LN1(x) in place and h = LN2(x). Q8: h as int8 hq with one scale per row in hs;

@@ -30,7 +30,9 @@ EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the 
 EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_layernorm_q8", "cohere_dec_w8_linear",
            "cohere_linear_bf16", "cohere_last_error", "cohere_version", "cohere_set_gemm_tile",
            "cohere_set_skinny_shape", "cohere_layernorm", "cohere_dwconv_bn_silu", "cohere_dwconv_bn_silu_q8",
-           "cohere_relpos_attention", "cohere_encoder_workspace_bytes", "cohere_encoder_layers")
+           "cohere_relpos_attention", "cohere_encoder_workspace_bytes", "cohere_encoder_layers", "cohere_dec_embed",
+           "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
+           "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -52,6 +54,13 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_dwconv_bn_silu": [P, P, P, P, P, P, P, P, I64, I64, I64, P],
         "cohere_dwconv_bn_silu_q8": [P, P, P, P, P, P, P, P, P, I64, I64, I64, P],
         "cohere_relpos_attention": [P, P, I64, P, P, P, I64, I64, I64, I64, I64, F, P, P],
+        "cohere_dec_embed": [P, I64, P, P, P, P, P, P, F, P, P, F, P, P, I64, P],
+        "cohere_dec_add_ln": [P, P, I64, P, P, F, P, I64, I64, P],
+        "cohere_dec_attention": [I32, P, I64, P, I64, P, P, P, I64, I64, F, I64, P, I64, P, P],
+        "cohere_dec_attention_q8": [I32, P, I64, P, I64, P, P, P, P, P, I64, I64, F, I64, P, I64, P, P],
+        "cohere_dec_pick": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P],
+        "cohere_dec_scatter_kv": [P, I64, P, P, P, P, I64, I64, I64, I64, P],
+        "cohere_dec_scatter_kv_q8": [P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P],
         "cohere_encoder_layers": [P, I64, P, I64, P, P, I64, P, P, I64, I64, I64, ctypes.c_double, I32, I32, I32, P,
                                   I64, P, I64, P],
     }
@@ -282,6 +291,77 @@ class _Ext:
             return
         self._call("cohere_linear_bf16", _ptr(x), x.stride(0), _ptr(w), _ptr(bias), _ptr(y), y.stride(0),
                    int(bool(relu)), M, w.shape[0], K, _stream())
+
+
+    # ---- decoder step (bindings.cpp:77-84) -------------------------------------------------------------------------
+
+    def dec_embed(self, active, tok, pos, emb, ptab, w0, b0, eps0, w1, b1, eps1, x, h):
+        """x = LN0(embed[tok[s]] + pos_table[pos[s]]), h = LN1(x) for s = active[r] (decoder_ops.cu:208-219)."""
+        _check(x.is_contiguous() and h.is_contiguous() and x.dtype == h.dtype == emb.dtype == torch.bfloat16,
+               "dec_embed: contiguous bf16 x, h")
+        _check(active.dtype == torch.int32 and tok.dtype == torch.int64 and pos.dtype == torch.int32,
+               "dec_embed: int32 active/pos, int64 tok")
+        rows, width = x.shape
+        _check(emb.shape[1] == width and ptab.shape[1] == width, "dec_embed: widths")
+        self._call("cohere_dec_embed", _ptr(active), rows, _ptr(tok), _ptr(pos), _ptr(emb), _ptr(ptab), _ptr(w0),
+                   _ptr(b0), float(eps0), _ptr(w1), _ptr(b1), float(eps1), _ptr(x), _ptr(h), width, _stream())
+
+    def dec_add_ln(self, x, y, w, b, eps, h):
+        """x = bf16(x + y) in place, h = LN(x) (decoder_ops.cu:221-233)."""
+        _check(x.is_contiguous() and h.is_contiguous() and y.stride(1) == 1, "dec_add_ln: contiguous x, h")
+        rows, width = x.shape
+        self._call("cohere_dec_add_ln", _ptr(x), _ptr(y), y.stride(0), _ptr(w), _ptr(b), float(eps), _ptr(h), rows,
+                   width, _stream())
+
+    def _att_checks(self, q, k, out, part, splits):
+        _check(k.dim() == 4 and k.shape[3] == 128 and k.is_contiguous() and q.stride(1) == 1 and out.is_contiguous(),
+               "dec_attention: caches (slots, H, T, 128) contiguous, q with unit column stride")
+        rows, H = q.shape[0], k.shape[1]
+        _check(splits == 1 or (part is not None and part.numel() >= rows * H * splits * 130),
+               "dec_attention: splits > 1 needs part")
+        return rows, H
+
+    def dec_attention(self, self_attn, active, q, k, v, n, scale, splits, part, out):
+        """softmax(q k^T scale) v of one new token per row over its slot's bf16 cache (decoder_ops.cu:235-262)."""
+        rows, H = self._att_checks(q, k, out, part, splits)
+        self._call("cohere_dec_attention", int(bool(self_attn)), _ptr(active), rows, _ptr(q), q.stride(0), _ptr(k),
+                   _ptr(v), _ptr(n), H, k.shape[2], float(scale), int(splits), _ptr(part),
+                   part.numel() if part is not None else 0, _ptr(out), _stream())
+
+    def dec_attention_q8(self, self_attn, active, q, k8, v8, ks, vs, n, scale, splits, part, out):
+        """dec_attention over int8 caches with one scale per 128-vector (decoder_ops.cu:264-290)."""
+        rows, H = self._att_checks(q, k8, out, part, splits)
+        _check(k8.dtype == torch.int8 and ks.dtype == torch.float32 and ks.is_contiguous() and vs.is_contiguous(),
+               "dec_attention_q8: int8 caches, fp32 scales")
+        self._call("cohere_dec_attention_q8", int(bool(self_attn)), _ptr(active), rows, _ptr(q), q.stride(0),
+                   _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs), _ptr(n), H, k8.shape[2], float(scale), int(splits),
+                   _ptr(part), part.numel() if part is not None else 0, _ptr(out), _stream())
+
+    def dec_pick(self, logits, active, dummy, tok, pos, finished, forced, plen, limit, out, pad, eos):
+        """Greedy choice, forced prompt and end bookkeeping per active slot (decoder_ops.cu:304-314)."""
+        _check(logits.is_contiguous() and logits.shape[1] % 8 == 0, "dec_pick: contiguous logits, V % 8 == 0")
+        _check(tok.dtype == torch.int64 and forced.dtype == torch.int64 and out.dtype == torch.int64 and
+               finished.dtype == torch.uint8, "dec_pick: dtypes")
+        rows, V = logits.shape
+        self._call("cohere_dec_pick", _ptr(logits), rows, V, _ptr(active), int(dummy), _ptr(tok), _ptr(pos),
+                   _ptr(finished), _ptr(forced), forced.shape[1], _ptr(plen), _ptr(limit), _ptr(out), out.shape[1],
+                   int(pad), int(eos), _stream())
+
+    def dec_scatter_kv(self, kv, slot_of, frame_of, ck, cv):
+        """Cross-attention keys/values of packed frames into their slots (decoder_ops.cu:316-327)."""
+        L, S, H, T = ck.shape[:4]
+        _check(kv.is_contiguous() and kv.shape[1] == L * 2 * H * 128 and ck.is_contiguous() and cv.is_contiguous(),
+               "dec_scatter_kv: shapes")
+        self._call("cohere_dec_scatter_kv", _ptr(kv), kv.shape[0], _ptr(slot_of), _ptr(frame_of), _ptr(ck),
+                   _ptr(cv), L, S, H, T, _stream())
+
+    def dec_scatter_kv_q8(self, kv, slot_of, frame_of, ck, cv, cks, cvs):
+        """The same into int8 caches with one scale per 128-vector (decoder_ops.cu:292-302)."""
+        L, S, H, T = ck.shape[:4]
+        _check(kv.is_contiguous() and kv.shape[1] == L * 2 * H * 128 and ck.dtype == torch.int8,
+               "dec_scatter_kv_q8: shapes")
+        self._call("cohere_dec_scatter_kv_q8", _ptr(kv), kv.shape[0], _ptr(slot_of), _ptr(frame_of), _ptr(ck),
+                   _ptr(cv), _ptr(cks), _ptr(cvs), L, S, H, T, _stream())
 
 
 _lib = load_library()

@@ -124,6 +124,63 @@ int cohere_relpos_attention(const uint16_t* qkv, const uint16_t* rk, int64_t rel
                             const uint16_t* bv, const int32_t* tiles, int64_t n_tiles, int64_t heads, int64_t head_dim,
                             int64_t rel_off, int64_t max_len, float scale, uint16_t* out, void* stream);
 
+/* ---- decoder step (reference kernels/csrc/decoder_ops.cu, dec_attn.cuh) ------------------------------------------
+ * Row r of a step works on slot active[r] (int32 [rows]) of the per-slot state: tok int64 [slots], pos int32
+ * [slots], and caches laid out (slots, heads, T, 128). */
+
+/* Replaces dec_embed (reference kernels/csrc/decoder_ops.cu:24-54, 208-219, bound at kernels/csrc/bindings.cpp:77):
+ * x = LN0(bf16(emb[tok[s]] + ptab[pos[s]])), h = LN1(x), bf16 [rows, width] contiguous; emb / ptab bf16 tables with
+ * `width` columns. width % 8 == 0, <= 2048. */
+int cohere_dec_embed(const int32_t* active, int64_t rows, const int64_t* tok, const int32_t* pos, const uint16_t* emb,
+                     const uint16_t* ptab, const uint16_t* w0, const uint16_t* b0, float eps0, const uint16_t* w1,
+                     const uint16_t* b1, float eps1, uint16_t* x, uint16_t* h, int64_t width, void* stream);
+
+/* Replaces dec_add_ln (reference kernels/csrc/decoder_ops.cu:56-83, 221-233, bound at kernels/csrc/bindings.cpp:78):
+ * x = bf16(x + y) in place (x [rows, width] contiguous, y row stride ldy), h = LN(x). */
+int cohere_dec_add_ln(uint16_t* x, const uint16_t* y, int64_t ldy, const uint16_t* w, const uint16_t* b, float eps,
+                      uint16_t* h, int64_t rows, int64_t width, void* stream);
+
+/* Replaces dec_attention (reference kernels/csrc/decoder_ops.cu:235-262, dec_attn.cuh:84-188, bound at
+ * kernels/csrc/bindings.cpp:80): out bf16 [rows, heads * 128] = softmax(q k^T scale) v for one new token per row.
+ * self != 0: q is the qkv projection [rows, ldq] (q | k | v, heads x 128 each), the new key and value are first
+ * written into the caches at position n[s] and attended as computed, with keys 0 .. n[s]-1 from the cache; self == 0:
+ * q [rows, ldq] over the slot's n[s] audio frames. Caches k, v bf16 (slots, heads, T, 128). splits > 1 splits each
+ * (row, head)'s keys over workgroups and needs part with rows x heads x splits x 130 floats. */
+int cohere_dec_attention(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
+                         uint16_t* k, uint16_t* v, const int32_t* n, int64_t heads, int64_t T, float scale,
+                         int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream);
+
+/* Replaces dec_attention_q8 (reference kernels/csrc/decoder_ops.cu:264-290, bound at kernels/csrc/bindings.cpp:81):
+ * as cohere_dec_attention over int8 caches k8, v8 (slots, heads, T, 128) with fp32 scales ks, vs (slots, heads, T),
+ * one per 128-vector; self-attention writes the new key and value quantized (absmax / 127, round half even) and
+ * attends to them unquantized. */
+int cohere_dec_attention_q8(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
+                            int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n, int64_t heads, int64_t T,
+                            float scale, int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream);
+
+/* Replaces dec_pick (reference kernels/csrc/decoder_ops.cu:106-159, 304-314, bound at kernels/csrc/bindings.cpp:83):
+ * per row (slot s = active[r], skipped when s == dummy or finished[s]): the first index of the maximum of logits bf16
+ * [rows, V]; at = pos[s] + 1; the token is forced[s, at] (int64 [slots, FP]) while at < plen[s], else the argmax;
+ * out[s, at] = tok[s] = token (out int64 [slots, OUT]); pos[s] = at; finished[s] = 1 at eos or at >= limit[s]
+ * outside the prompt. V % 8 == 0. */
+int cohere_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active, int64_t dummy,
+                    int64_t* tok, int32_t* pos, uint8_t* finished, const int64_t* forced, int64_t FP,
+                    const int32_t* plen, const int32_t* limit, int64_t* out, int64_t OUT, int64_t pad, int64_t eos,
+                    void* stream);
+
+/* Replaces dec_scatter_kv (reference kernels/csrc/decoder_ops.cu:163-175, 316-327, bound at
+ * kernels/csrc/bindings.cpp:84): kv bf16 [rows, L x 2 x H x 128] (per layer: keys of every head, then values) of
+ * packed encoder frames, row i = frame frame_of[i] of slot slot_of[i], into caches ck, cv (L, S, H, T, 128). */
+int cohere_dec_scatter_kv(const uint16_t* kv, int64_t rows, const int32_t* slot_of, const int32_t* frame_of,
+                          uint16_t* ck, uint16_t* cv, int64_t L, int64_t S, int64_t H, int64_t T, void* stream);
+
+/* Replaces dec_scatter_kv_q8 (reference kernels/csrc/decoder_ops.cu:177-204, 292-302, bound at
+ * kernels/csrc/bindings.cpp:82): as cohere_dec_scatter_kv into int8 caches with one fp32 scale per 128-vector
+ * (cks, cvs (L, S, H, T)). */
+int cohere_dec_scatter_kv_q8(const uint16_t* kv, int64_t rows, const int32_t* slot_of, const int32_t* frame_of,
+                             int8_t* ck, int8_t* cv, float* cks, float* cvs, int64_t L, int64_t S, int64_t H,
+                             int64_t T, void* stream);
+
 /* Number of per-layer tensors of cohere_encoder_layers (the reference's enum F, kernels/csrc/encoder_loop.cpp:34-44) */
 enum { COHERE_ENC_N_FIELDS = 53 };
 

@@ -28,6 +28,14 @@ Function -> reference -> what pins it (tests/test_oracle.py unless noted):
   relpos_attention      kernels/csrc/encoder_ops.cu:82-337  transformers' ParakeetEncoderAttention (rel_shift form)
                                                         in float32; with a zero table and zero biases, softmax
                                                         attention in float64
+  dec_embed, dec_add_ln kernels/csrc/decoder_ops.cu:24-83  torch float64 LayerNorm of the bf16 sums
+  dec_attention         kernels/csrc/dec_attn.cuh:84-188  torch scaled_dot_product_attention in float64 over the
+                                                        dequantized caches; the new key/value written at pos
+  dec_pick              kernels/csrc/decoder_ops.cu:106-159  torch.argmax (first index of the maximum) + the
+                                                        bookkeeping rules written out by hand in the test
+  dec_scatter_kv        kernels/csrc/decoder_ops.cu:163-204  q8_rows-style absmax round trip per 128-vector
+  decoder_step          kernels/stream_decoder.py:176-199  transformers' CohereAsrDecoder (float32, one token per
+                                                        slot with its own cache) on the dequantized weights
   encoder_layers_int8   kernels/csrc/encoder_loop.cpp:63-99  transformers' ParakeetEncoderBlock in float32 on the
                                                         dequantized weights (within the int8 activation error)
 """
@@ -67,6 +75,12 @@ def lib() -> ctypes.CDLL:
         _lib.orc_layernorm.argtypes = [p, i64, p, p, ctypes.c_float, p, p, ctypes.c_float, p, i64, i64, i64]
         _lib.orc_dwconv_bn_silu.argtypes = [p, p, p, p, p, p, p, p, i64, i64]
         _lib.orc_relpos_attention.argtypes = [p, p, i64, p, p, p, p, i64, i64, i64, i64, ctypes.c_float, p]
+        _lib.orc_dec_embed.argtypes = [p, i64, p, p, p, p, p, p, ctypes.c_float, p, p, ctypes.c_float, p, p, i64]
+        _lib.orc_dec_add_ln.argtypes = [p, p, i64, p, p, ctypes.c_float, p, i64, i64]
+        _lib.orc_dec_attention.argtypes = [ctypes.c_int, ctypes.c_int, p, i64, p, i64, p, p, p, p, p, p, p, i64, i64,
+                                           ctypes.c_float, p]
+        _lib.orc_dec_pick.argtypes = [p, i64, i64, p, i64, p, p, p, p, i64, p, p, p, i64, i64]
+        _lib.orc_dec_scatter_kv.argtypes = [ctypes.c_int, p, i64, p, p, p, p, p, p, p, p, i64, i64, i64, i64]
         _lib.orc_gemm_i8.argtypes = [p, i64, p, i64, i64, p, i64, p, p, p, i64, ctypes.c_int, p, i64, ctypes.c_float,
                                      p, i64, i64, i64, i64, i64, p, ctypes.c_int]
         _lib.orc_gemm_i8.restype = ctypes.c_int
@@ -330,3 +344,92 @@ def encoder_layers_int8(x, layers, eps, lengths, rel_off, scale, group=256, qgro
         else:
             x, _ = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4])
     return x
+
+
+# ---- the decoder step (row a13) --------------------------------------------------------------------------------------
+# Arrays are numpy, modified in place like the kernels' outputs; bf16 as uint16 bits.
+
+def _ln_args(ln):
+    w, b, eps = ln
+    return _p(_c(w, np.uint16)), _p(_c(b, np.uint16)), float(eps)
+
+
+def dec_embed(active, tok, pos, emb, ptab, ln0, ln1):
+    """decoder_ops.cu:24-54: (x, h) bf16 bits [rows, width]."""
+    rows, width = len(active), emb.shape[1]
+    x, h = np.empty((rows, width), np.uint16), np.empty((rows, width), np.uint16)
+    lib().orc_dec_embed(_p(_c(active, np.int32)), rows, _p(_c(tok, np.int64)), _p(_c(pos, np.int32)),
+                        _p(_c(emb, np.uint16)), _p(_c(ptab, np.uint16)), *_ln_args(ln0), *_ln_args(ln1), _p(x), _p(h),
+                        width)
+    return x, h
+
+
+def dec_add_ln(x, y, ln):
+    """decoder_ops.cu:56-83: x = bf16(x + y) in place (x must be a C-contiguous uint16 array); returns h."""
+    assert x.dtype == np.uint16 and x.flags.c_contiguous
+    y = _c(y, np.uint16)
+    h = np.empty_like(x)
+    lib().orc_dec_add_ln(_p(x), _p(y), y.shape[1], *_ln_args(ln), _p(h), x.shape[0], x.shape[1])
+    return h
+
+
+def dec_attention(self_attn, active, q, n, scale, k=None, v=None, k8=None, v8=None, ks=None, vs=None):
+    """dec_attn.cuh:84-188 over one layer's caches (slots, H, T, 128): bf16 (k, v) or int8 (k8, v8, ks, vs), updated
+    in place for self-attention. Returns out bf16 bits [rows, H * 128]."""
+    q = _c(q, np.uint16)
+    q8 = k8 is not None
+    caches = (k8, v8, ks, vs) if q8 else (k, v)
+    for c in caches:
+        assert c.flags.c_contiguous
+    H, T = (k8 if q8 else k).shape[1:3]
+    rows = q.shape[0]
+    out = np.empty((rows, H * 128), np.uint16)
+    lib().orc_dec_attention(int(self_attn), int(q8), _p(_c(active, np.int32)), rows, _p(q), q.shape[1],
+                            _p(None if q8 else k), _p(None if q8 else v), _p(k8), _p(v8), _p(ks), _p(vs),
+                            _p(_c(n, np.int32)), H, T, scale, _p(out))
+    return out
+
+
+def dec_pick(logits, active, dummy, tok, pos, finished, forced, plen, limit, out, eos):
+    """decoder_ops.cu:106-159, the state arrays (numpy, contiguous) updated in place."""
+    logits = _c(logits, np.uint16)
+    for a in (tok, pos, finished, out):
+        assert a.flags.c_contiguous
+    lib().orc_dec_pick(_p(logits), logits.shape[0], logits.shape[1], _p(_c(active, np.int32)), dummy, _p(tok),
+                       _p(pos), _p(finished), _p(_c(forced, np.int64)), forced.shape[1], _p(_c(plen, np.int32)),
+                       _p(_c(limit, np.int32)), _p(out), out.shape[1], eos)
+
+
+def dec_scatter_kv(kv, slot_of, frame_of, ck=None, cv=None, ck8=None, cv8=None, cks=None, cvs=None):
+    """decoder_ops.cu:163-204 into caches (L, S, H, T, 128), in place."""
+    kv = _c(kv, np.uint16)
+    q8 = ck8 is not None
+    L, S, H, T = (ck8 if q8 else ck).shape[:4]
+    lib().orc_dec_scatter_kv(int(q8), _p(kv), kv.shape[0], _p(_c(slot_of, np.int32)), _p(_c(frame_of, np.int32)),
+                             _p(ck), _p(cv), _p(ck8), _p(cv8), _p(cks), _p(cvs), L, S, H, T)
+
+
+def decoder_step(W, st, b, int8=True):
+    """kernels/stream_decoder.py:176-199 (StreamDecoder._step) for the first b rows of st["active"], every step of it
+    by the functions above and the projections a11 / a12. W: weights (numpy; see tests/decoder_helpers.py); st: the
+    slot state and caches (numpy, updated in place). Returns the head's logits (bf16 bits [b, V])."""
+    act = st["active"][:b]
+    x, hn = dec_embed(act, st["tok"], st["pos"], W["embed"], W["pos_table"], W["emb_ln"], W["layers"][0]["ln1"])
+    lin = lambda a, name, ly, relu=False: (  # noqa: E731
+        dec_w8_linear(a, *ly[name + "_w8"], ly[name + "_b"], relu) if int8 and name + "_w8" in ly
+        else linear_bf16(a, ly[name + "_w"], ly[name + "_b"], relu))
+    L = len(W["layers"])
+    for i, ly in enumerate(W["layers"]):
+        qkv = lin(hn, "qkv", ly)
+        a = dec_attention(True, act, qkv, st["pos"], W["scale"], k8=st["self_k8"][i], v8=st["self_v8"][i],
+                          ks=st["self_ks"][i], vs=st["self_vs"][i])
+        hn = dec_add_ln(x, lin(a, "o", ly), ly["ln2"])
+        a = dec_attention(False, act, lin(hn, "cq", ly), st["cross_len"], W["scale"], k8=st["cross_k8"][i],
+                          v8=st["cross_v8"][i], ks=st["cross_ks"][i], vs=st["cross_vs"][i])
+        hn = dec_add_ln(x, lin(a, "co", ly), ly["ln3"])
+        f = lin(lin(hn, "fc1", ly, relu=True), "fc2", ly)
+        hn = dec_add_ln(x, f, W["layers"][i + 1]["ln1"] if i + 1 < L else W["final_ln"])
+    logits = lin(hn, "head", W)
+    dec_pick(logits, act, st["dummy"], st["tok"], st["pos"], st["finished"], st["forced"], st["plen"], st["limit"],
+             st["out"], W["eos"])
+    return logits

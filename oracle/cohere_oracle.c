@@ -409,6 +409,168 @@ void orc_relpos_attention(const uint16_t* qkv, const uint16_t* rk, int64_t rel_r
   }
 }
 
+/* ---- the decoder step's other kernels (row a13) ------------------------------------------------------------------ */
+
+/* kernels/csrc/decoder_ops.cu:24-54: x = LN0(bf16(emb[tok[s]] + ptab[pos[s]])), h = LN1(x) for s = active[r] */
+void orc_dec_embed(const int32_t* active, int64_t rows, const int64_t* tok, const int32_t* pos, const uint16_t* emb,
+                   const uint16_t* ptab, const uint16_t* w0, const uint16_t* b0, float eps0, const uint16_t* w1,
+                   const uint16_t* b1, float eps1, uint16_t* x, uint16_t* h, int64_t width) {
+  float* v = (float*)malloc(sizeof(float) * width * 2);
+  float* o = v + width;
+  for (int64_t r = 0; r < rows; ++r) {
+    const int s = active[r];
+    for (int64_t c = 0; c < width; ++c) v[c] = round_bf(bf2f(emb[tok[s] * width + c]) + bf2f(ptab[(int64_t)pos[s] * width + c]));
+    ln_row(v, width, w0, b0, eps0, o);
+    for (int64_t c = 0; c < width; ++c) x[r * width + c] = f2bf(o[c]);
+    memcpy(v, o, sizeof(float) * width);
+    ln_row(v, width, w1, b1, eps1, o);
+    for (int64_t c = 0; c < width; ++c) h[r * width + c] = f2bf(o[c]);
+  }
+  free(v);
+}
+
+/* kernels/csrc/decoder_ops.cu:56-83: x = bf16(x + y), h = LN(x) */
+void orc_dec_add_ln(uint16_t* x, const uint16_t* y, int64_t ldy, const uint16_t* w, const uint16_t* b, float eps,
+                    uint16_t* h, int64_t rows, int64_t width) {
+  float* v = (float*)malloc(sizeof(float) * width * 2);
+  float* o = v + width;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c = 0; c < width; ++c) {
+      v[c] = round_bf(bf2f(x[r * width + c]) + bf2f(y[r * ldy + c]));
+      x[r * width + c] = f2bf(v[c]);
+    }
+    ln_row(v, width, w, b, eps, o);
+    for (int64_t c = 0; c < width; ++c) h[r * width + c] = f2bf(o[c]);
+  }
+  free(v);
+}
+
+/* kernels/csrc/dec_attn.cuh:38-58 store16_q8: a 128-vector as int8 with scale absmax / 127 (1 for a zero vector) */
+static void q8_vec(const float* f, int8_t* q, float* scale) {
+  float mx = 0.f;
+  for (int k = 0; k < 128; ++k) mx = fmaxf(mx, fabsf(f[k]));
+  const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
+  for (int k = 0; k < 128; ++k) q[k] = (int8_t)rintf(fminf(fmaxf(f[k] * inv, -127.f), 127.f));
+  *scale = sc;
+}
+
+/* kernels/csrc/dec_attn.cuh:84-188 (attend_item) for every row and head: softmax(q k^T * scale) v over the slot's
+ * keys. self: the new key and value (columns H*128 and 2*H*128 of q's row) are written at position n[s] (int8: by
+ * q8_vec) and attended unquantized, keys 0 .. n[s]-1 come from the cache; cross: keys 0 .. n[s]-1. Cached values are
+ * dequantized as the kernel does (fp32 int8 * scale). Scores: s_j = fp32(q . k_j) * scale; the softmax in fp64 in one
+ * pass (the kernel runs it online in fp32 per key group; the order of the sums is not restated). q8 == 0: bf16
+ * caches k, v. */
+void orc_dec_attention(int self, int q8, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
+                       uint16_t* k, uint16_t* v, int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n,
+                       int64_t H, int64_t T, float scale, uint16_t* out) {
+  const int64_t HD = 128;
+  for (int64_t r = 0; r < rows; ++r) {
+    const int s = active[r];
+    for (int64_t h = 0; h < H; ++h) {
+      const int64_t vec0 = ((int64_t)s * H + h) * T;
+      const int nk = n[s];
+      float qf[128], kn[128], vn[128], kk[128];
+      double acc[128];
+      for (int d = 0; d < HD; ++d) qf[d] = bf2f(q[r * ldq + h * HD + d]);
+      const int total = nk + (self ? 1 : 0);
+      double* sc = (double*)malloc(sizeof(double) * (total > 0 ? total : 1));
+      if (self) {
+        for (int d = 0; d < HD; ++d) {
+          kn[d] = bf2f(q[r * ldq + H * HD + h * HD + d]);
+          vn[d] = bf2f(q[r * ldq + 2 * H * HD + h * HD + d]);
+        }
+      }
+      double mx = -INFINITY;
+      for (int j = 0; j < total; ++j) {
+        const int is_new = self && j == nk;
+        if (is_new) {
+          memcpy(kk, kn, sizeof kk);
+        } else if (q8) {
+          for (int d = 0; d < HD; ++d) kk[d] = (float)k8[(vec0 + j) * HD + d] * ks[vec0 + j];
+        } else {
+          for (int d = 0; d < HD; ++d) kk[d] = bf2f(k[(vec0 + j) * HD + d]);
+        }
+        double dot = 0.0;
+        for (int d = 0; d < HD; ++d) dot += (double)qf[d] * (double)kk[d];
+        sc[j] = (double)((float)dot * scale);
+        if (sc[j] > mx) mx = sc[j];
+      }
+      double l = 0.0;
+      for (int d = 0; d < HD; ++d) acc[d] = 0.0;
+      for (int j = 0; j < total; ++j) {
+        const double e = exp(sc[j] - mx);
+        l += e;
+        const int is_new = self && j == nk;
+        for (int d = 0; d < HD; ++d) {
+          const float vv = is_new ? vn[d] : (q8 ? (float)v8[(vec0 + j) * HD + d] * vs[vec0 + j] : bf2f(v[(vec0 + j) * HD + d]));
+          acc[d] += e * (double)vv;
+        }
+      }
+      for (int d = 0; d < HD; ++d) out[r * H * HD + h * HD + d] = f2bf((float)(acc[d] / l));
+      free(sc);
+      if (self) {  /* the cache write (after the attention reads: the new position is not read from the cache) */
+        if (q8) {
+          q8_vec(kn, k8 + (vec0 + nk) * HD, ks + vec0 + nk);
+          q8_vec(vn, v8 + (vec0 + nk) * HD, vs + vec0 + nk);
+        } else {
+          for (int d = 0; d < HD; ++d) {
+            k[(vec0 + nk) * HD + d] = f2bf(kn[d]);
+            v[(vec0 + nk) * HD + d] = f2bf(vn[d]);
+          }
+        }
+      }
+    }
+  }
+}
+
+/* kernels/csrc/decoder_ops.cu:106-159 dec_pick */
+void orc_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active, int64_t dummy, int64_t* tok,
+                  int32_t* pos, uint8_t* finished, const int64_t* forced, int64_t FP, const int32_t* plen,
+                  const int32_t* limit, int64_t* out, int64_t OUT, int64_t eos) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const int s = active[r];
+    if (s == dummy || finished[s]) continue;
+    float best = -INFINITY;
+    int64_t arg = 0;
+    for (int64_t i = 0; i < V; ++i) {
+      const float v = bf2f(logits[r * V + i]);
+      if (v > best) {
+        best = v;
+        arg = i;
+      }
+    }
+    const int at = pos[s] + 1;
+    const int in_prompt = at < plen[s];
+    const int64_t nt = in_prompt ? forced[(int64_t)s * FP + at] : arg;
+    out[(int64_t)s * OUT + at] = nt;
+    tok[s] = nt;
+    pos[s] = at;
+    finished[s] = (!in_prompt && (nt == eos || at >= limit[s])) ? 1 : 0;
+  }
+}
+
+/* kernels/csrc/decoder_ops.cu:163-204 dec_scatter_kv(_q8): row i of kv (L x 2 x H x 128 per row) into slot
+ * slot_of[i], frame frame_of[i] of the caches (L, S, H, T, 128); q8 by q8_vec per 128-vector */
+void orc_dec_scatter_kv(int q8, const uint16_t* kv, int64_t rows, const int32_t* slot_of, const int32_t* frame_of,
+                        uint16_t* ck, uint16_t* cv, int8_t* ck8, int8_t* cv8, float* cks, float* cvs, int64_t L,
+                        int64_t S, int64_t H, int64_t T) {
+  const int64_t HD = 128;
+  float f[128];
+  for (int64_t r = 0; r < rows; ++r)
+    for (int64_t l = 0; l < L; ++l)
+      for (int kvi = 0; kvi < 2; ++kvi)
+        for (int64_t h = 0; h < H; ++h) {
+          const uint16_t* src = kv + r * L * 2 * H * HD + ((l * 2 + kvi) * H + h) * HD;
+          const int64_t vec = ((l * S + slot_of[r]) * H + h) * T + frame_of[r];
+          if (q8) {
+            for (int d = 0; d < HD; ++d) f[d] = bf2f(src[d]);
+            q8_vec(f, (kvi ? cv8 : ck8) + vec * HD, (kvi ? cvs : cks) + vec);
+          } else {
+            memcpy((kvi ? cv : ck) + vec * HD, src, HD * 2);
+          }
+        }
+}
+
 /* bf16 <-> fp32 helpers exported for the Python side of the checker */
 void orc_f32_to_bf16(const float* f, uint16_t* h, int64_t n) {
   for (int64_t i = 0; i < n; ++i) h[i] = f2bf(f[i]);
