@@ -63,7 +63,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   constexpr int MAXB = (W8 ? 16 : 8) / NS;  // K blocks per wave held in registers at once (64 VGPRs of weights)
   constexpr int COLS = NS * 16, LDR = COLS + 4;
   __shared__ __attribute__((aligned(16))) float red[NW][MB * 16][LDR];
-  const int n0 = blockIdx.x * COLS;
+  const int n0 = blockIdx.x * COLS, m_base = blockIdx.y * MB * 16;  // grid.y > 1: the rows split over workgroups
   const int lane = threadIdx.x & 63, wave = wave_id(), h = lane >> 4, c16 = lane & 15;
   const int nkb = p.K / KB;  // wave w takes blocks w, w + NW, ...
 
@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const int m = min(mb * 16 + c16, p.M - 1);
+        const int m = min(m_base + mb * 16 + c16, p.M - 1);
         const uint16_t* xr = p.X + (int64_t)m * p.ldx + k;
         v8bf x0, x1;
         if constexpr (W8) {
@@ -142,11 +142,12 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
     for (int mb = 0; mb < MB; ++mb)
       *reinterpret_cast<v4f*>(&red[wave][mb * 16 + c16][s * 16 + h * 4]) = acc[s][mb];
   __syncthreads();
-  for (int i = threadIdx.x; i < p.M * COLS; i += NW * 64) {
-    const int m = i / COLS, c = i % COLS, n = n0 + c;
-    float v = red[0][m][c];
+  const int rows = min(p.M - m_base, MB * 16);
+  for (int i = threadIdx.x; i < rows * COLS; i += NW * 64) {
+    const int r = i / COLS, c = i % COLS, n = n0 + c, m = m_base + r;
+    float v = red[0][r][c];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) v += red[w][m][c];
+    for (int w = 1; w < NW; ++w) v += red[w][r][c];
     if constexpr (W8) v = __builtin_fmaf(v, p.sw[n], p.bias ? bf2f(p.bias[n]) : 0.f);
     else if (p.bias) v = v + bf2f(p.bias[n]);
     if (RELU) v = fmaxf(v, 0.f);
@@ -158,8 +159,14 @@ int g_skinny_override = -1;  // (NS << 8) | NW, tuning hook
 
 template <int NS, int NW, bool W8, bool RELU>
 void launch_rows(const SkinnyArgs& p, hipStream_t s) {
-  const int grid = p.N / (NS * 16);
-  switch ((p.M + 15) / 16) {
+  const int grid = p.N / (NS * 16), mblocks = (p.M + 15) / 16;
+  if (grid * mblocks <= 512 && mblocks > 1) {
+    // few channel strips: one workgroup per (strip, 16 rows), so that every CU streams (the strip is read once per
+    // 16 rows, the repeats mostly from L2 / MALL)
+    skinny_kernel<1, NS, NW, W8, RELU><<<dim3(grid, mblocks), NW * 64, 0, s>>>(p);
+    return;
+  }
+  switch (mblocks) {
     case 1: skinny_kernel<1, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
     case 2: skinny_kernel<2, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
     case 3: skinny_kernel<3, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;

@@ -71,9 +71,10 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
 
 // ---- attention of one new token per row ---------------------------------------------------------------------------
 // A workgroup of 256 threads per (row, head, split): 32 groups of 8 lanes, each lane 16 of the 128 dims, each group
-// streaming every 32nd key of the split (two in flight). Per key: the group's partial dot products meet through
-// three lane shuffles; the online softmax runs in fp32 per group; the 32 groups are combined through LDS at the end
-// (or, with several splits, written as partials (o[128], max, sum) for dec_combine).
+// taking every 32nd key of the split, 8 (int8) or 4 (bf16) keys per pass with all their loads in flight at once. Per
+// key the group's partial dot products meet through three lane shuffles; the online softmax runs in fp32 per group,
+// one rescale per pass; the 32 groups are combined through LDS at the end (or, with several splits, written as
+// partials (o[128], max, sum) for dec_combine).
 struct DecAttnArgs {
   const int32_t* active;
   const uint16_t* q;  // (rows, ldq): head h at column h * 128 (self: q | k | v of the new token)
@@ -91,7 +92,7 @@ struct DecAttnArgs {
   float* part;        // (rows, H, splits, 130) when split
 };
 
-constexpr int AG = 32;  // key groups per workgroup
+constexpr int AG = 32;  // key groups per workgroup (8 lanes each: 256 threads)
 
 DEVI void load16_bf(const uint16_t* p, float (&f)[16]) {
   const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
@@ -108,6 +109,25 @@ DEVI void load16_q8(const int8_t* p, float s, float (&f)[16]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
   for (int k = 0; k < 16; ++k) f[k] = (float)(int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xff) * s;
+}
+
+DEVI void unpack_q8(const uint4& u, float s, float (&f)[16]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int k = 0; k < 16; ++k) f[k] = (float)(int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xff);
+  if (s != 1.f) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) f[k] *= s;
+  }
+}
+
+DEVI void unpack_bf(const uint4& a, const uint4& b, float (&f)[16]) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
 }
 
 // group-of-8 reductions (lanes 8g .. 8g+7 of a wave)
@@ -155,7 +175,7 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
 }
 
 template <bool SELF, bool Q8>
-__global__ void __launch_bounds__(256) dec_attention_kernel(const DecAttnArgs p) {
+__global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs p) {
   __shared__ float sm[AG], sl[AG];
   __shared__ float sacc[AG][HD + 4];
   const int r = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
@@ -188,28 +208,58 @@ __global__ void __launch_bounds__(256) dec_attention_kernel(const DecAttnArgs p)
     attend_one(q, kn, vn, p.scale, m, l, acc);
   }
   const int chunk = (n + nsp - 1) / nsp, start = sp * chunk, end = min(n, start + chunk);
-  int j = start + grp;
-  auto key = [&](int jj, float (&kk)[16], float (&vv)[16]) {
-    const int64_t vec = vec0 + jj;
-    if constexpr (Q8) {
-      load16_q8(p.k8 + vec * HD + gl * 16, p.ks[vec], kk);
-      load16_q8(p.v8 + vec * HD + gl * 16, p.vs[vec], vv);
-    } else {
-      load16_bf(p.k + vec * HD + gl * 16, kk);
-      load16_bf(p.v + vec * HD + gl * 16, vv);
+  // each group takes KB keys per pass (every 32nd key), all loads issued before any use: one memory round trip per
+  // KB keys; then one softmax update for the block
+  constexpr int KB = Q8 ? 8 : 4;
+  for (int j0 = start + grp; j0 < end; j0 += KB * AG) {
+    uint4 kr[KB][Q8 ? 1 : 2], vr[KB][Q8 ? 1 : 2];
+    float ksc[KB], vsc[KB];
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int jj = j0 + i * AG;
+      const int64_t vec = vec0 + (jj < end ? jj : start);
+      if constexpr (Q8) {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + vec * HD + gl * 16);
+        vr[i][0] = *reinterpret_cast<const uint4*>(p.v8 + vec * HD + gl * 16);
+        ksc[i] = p.ks[vec];
+        vsc[i] = p.vs[vec];
+      } else {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16);
+        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16 + 8);
+        vr[i][0] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16);
+        vr[i][1] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16 + 8);
+      }
     }
-  };
-  for (; j + AG < end; j += 2 * AG) {
-    float k0[16], v0[16], k1[16], v1[16];
-    key(j, k0, v0);
-    key(j + AG, k1, v1);
-    attend_one(q, k0, v0, p.scale, m, l, acc);
-    attend_one(q, k1, v1, p.scale, m, l, acc);
-  }
-  if (j < end) {
-    float k0[16], v0[16];
-    key(j, k0, v0);
-    attend_one(q, k0, v0, p.scale, m, l, acc);
+    float sc[KB], mb = m;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      float kk[16];
+      if constexpr (Q8) unpack_q8(kr[i][0], 1.f, kk);  // the integers; the key's scale multiplies the dot product
+      else unpack_bf(kr[i][0], kr[i][1], kk);
+      float d = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) d = __builtin_fmaf(q[k], kk[k], d);
+      d = group_sum(d);
+      if constexpr (Q8) d *= ksc[i];
+      sc[i] = j0 + i * AG < end ? d * p.scale : -INFINITY;
+      mb = fmaxf(mb, sc[i]);
+    }
+    const float a = __expf(m - mb);
+    l *= a;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] *= a;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const float e = __expf(sc[i] - mb);
+      l += e;
+      float vv[16];
+      if constexpr (Q8) unpack_q8(vr[i][0], 1.f, vv);  // the integers; the value's scale goes into the weight
+      else unpack_bf(vr[i][0], vr[i][1], vv);
+      const float ew = Q8 ? e * vsc[i] : e;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(ew, vv[k], acc[k]);
+    }
+    m = mb;
   }
   // combine the groups: weights exp(m_g - M)
   if (gl == 0) {
@@ -426,11 +476,11 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)rows, (unsigned)p.H, (unsigned)splits);
   if (self) {
-    if (q8) dec_attention_kernel<true, true><<<grid, 256, 0, s>>>(p);
-    else dec_attention_kernel<true, false><<<grid, 256, 0, s>>>(p);
+    if (q8) dec_attention_kernel<true, true><<<grid, AG * 8, 0, s>>>(p);
+    else dec_attention_kernel<true, false><<<grid, AG * 8, 0, s>>>(p);
   } else {
-    if (q8) dec_attention_kernel<false, true><<<grid, 256, 0, s>>>(p);
-    else dec_attention_kernel<false, false><<<grid, 256, 0, s>>>(p);
+    if (q8) dec_attention_kernel<false, true><<<grid, AG * 8, 0, s>>>(p);
+    else dec_attention_kernel<false, false><<<grid, AG * 8, 0, s>>>(p);
   }
   if (splits > 1) dec_combine_kernel<<<dim3((unsigned)rows, (unsigned)p.H), HD, 0, s>>>(p.part, (int)splits, p.out, p.H);
   return cohere::check_launch(name);
