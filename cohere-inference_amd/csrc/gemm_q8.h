@@ -71,7 +71,7 @@ struct Tile {
   static constexpr int KSTEP = MS == 16 ? (SPARSE ? 128 : 64) : (SPARSE ? 64 : 32);
   static constexpr int SPS = 128 / KSTEP;
   static constexpr int RPL = MS == 16 ? 4 : 16;
-  static constexpr bool PF = NW <= 4;  // one wave per SIMD: double-buffer the fragments within the wave
+  static constexpr bool PF = NW <= 4 && MI * NI <= 32;  // fragment double-buffering (register budget)
   static constexpr int X_STAGE = BM * 128;
   static constexpr int W_STAGE = SPARSE ? BN * 64 : BN * 128;
   static constexpr int E_STAGE = SPARSE ? BN * 16 : 0;
@@ -161,8 +161,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   const bool half_last = (K & 127) != 0;  // dense only: the last tile holds 64 K
   const int NSTEPS = K / KSTEP;
 
-  // the epilogue's per-row / per-channel values, and (grouped) every group's token scales, copied to LDS before the
-  // first DMA; the first barrier publishes them
+  // the epilogue's per-row / per-channel values and (grouped) every group's token scales live in LDS past the
+  // pipeline buffers; the first barrier publishes them
   float* pS = reinterpret_cast<float*>(smem + T::PIPE);
   float* pW = pS + BM;
   float* pB = pW + BN;
@@ -171,15 +171,43 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   const int group_steps = GS > 0 ? GS : (GROUPED ? p.group / KSTEP : 1);
   const int G = GROUPED ? K / p.group : 1;
   const bool scales_in_lds = GROUPED && G <= T::GMAX;
-  if constexpr (EPI != EPI_I32) {
-    for (int i = tid; i < BM + 2 * BN; i += NT) {
-      float v;
-      if (i < BM) v = GROUPED ? 1.f : p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
-      else if (i < BM + BN) v = p.sw[n0 + i - BM];
-      else v = p.bias ? bf2f(p.bias[n0 + i - BM - BN]) : 0.f;
-      pS[i] = v;
+  // per-row / per-channel epilogue values: loaded into registers between the first stage's DMA and the others (so
+  // their latency overlaps the transfers), stored to LDS once the first stage has landed
+  // (each kind in its own registers, unconverted: using a loaded value before the first wait would make the compiler
+  // wait for the first stage's transfers too)
+  constexpr int NPM = (BM + NT - 1) / NT, NPN = (BN + NT - 1) / NT;
+  float psx[NPM], psw[NPN];
+  uint16_t pbb[NPN];
+  auto load_params = [&]() {
+    if constexpr (EPI != EPI_I32) {
+#pragma unroll
+      for (int x = 0; x < NPM; ++x) {
+        const int i = tid + x * NT;
+        if (!GROUPED && i < BM) psx[x] = p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
+      }
+#pragma unroll
+      for (int x = 0; x < NPN; ++x) {
+        const int i = tid + x * NT;
+        if (i < BN) {
+          psw[x] = p.sw[n0 + i];
+          if (p.bias) pbb[x] = p.bias[n0 + i];
+        }
+      }
     }
-  }
+  };
+  auto store_params = [&]() {
+    if constexpr (EPI != EPI_I32) {
+#pragma unroll
+      for (int x = 0; x < NPM; ++x)
+        if (tid + x * NT < BM) pS[tid + x * NT] = GROUPED ? 1.f : psx[x];
+#pragma unroll
+      for (int x = 0; x < NPN; ++x)
+        if (tid + x * NT < BN) {
+          pW[tid + x * NT] = psw[x];
+          pB[tid + x * NT] = p.bias ? bf2f(pbb[x]) : 0.f;
+        }
+    }
+  };
   if (scales_in_lds) {
     for (int i = tid; i < G * BM; i += NT) {
       const int g = i / BM, r = i % BM;
@@ -339,16 +367,32 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   };
   // before reading step u, the first of stage t = u / SPS: stage t landed everywhere and stage t - 1 is free, so
   // stage t - 1 + ST can stream into its buffer
+  // Dense: the freed buffer's next transfer is issued after the step's matrix instructions (flush_issue), so that a
+  // busy load unit never holds up the matrix cores at the start of a step (measured: 5 % faster dense loops; the
+  // sparse tiles, with one step per stage, are faster issuing at once).
+  int pending = -1;
   auto enter_stage = [&](int t) {
     wait_stages<LPS, ST>(min(KT - 1 - t, ST - 2));
     lds_barrier();
-    if (t - 1 + ST < KT) issue((t - 1 + ST) % ST, t - 1 + ST);
+    if (t - 1 + ST < KT) {
+      if constexpr (SPARSE) issue((t - 1 + ST) % ST, t - 1 + ST);
+      else pending = t - 1 + ST;
+    }
+  };
+  auto flush_issue = [&]() {
+    if (pending >= 0) {
+      issue(pending % ST, pending);
+      pending = -1;
+    }
   };
 
+  issue(0, 0);
+  load_params();
 #pragma unroll
-  for (int s = 0; s < ST; ++s)
+  for (int s = 1; s < ST; ++s)
     if (s < KT) issue(s, s);
   wait_stages<LPS, ST>(min(KT - 1, ST - 1));
+  store_params();
   lds_barrier();
   if constexpr (GS > 0) {
     // whole groups of GS steps, unrolled: the fold sits at each group's first step (not the first group's), so the
@@ -365,10 +409,12 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
             load_frags(F[(s + 1) & 1], u + 1);
           }
           mma_step(F[s & 1], decltype(fold_tag)::value && s == 0, g - 1);
+          flush_issue();
         } else {
           if (u > 0 && s % SPS == 0) enter_stage(u / SPS);
           load_frags(F[0], u);
           mma_step(F[0], decltype(fold_tag)::value && s == 0, g - 1);
+          flush_issue();
         }
       }
     };
@@ -384,12 +430,14 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
         load_frags(F1, u + 1);
       }
       mma(F0);
+      flush_issue();
       if (u + 1 < NSTEPS) {
         if (u + 2 < NSTEPS) {
           if ((u + 2) % SPS == 0) enter_stage((u + 2) / SPS);
           load_frags(F0, u + 2);
         }
         mma(F1);
+        flush_issue();
       }
     }
   } else {
@@ -399,6 +447,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       if (u > 0 && u % SPS == 0) enter_stage(u / SPS);
       load_frags(F0, u);
       mma(F0);
+      flush_issue();
     }
   }
 
@@ -443,37 +492,56 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       }
     };
     if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID || EPI == EPI_GLU) {
+      // the tile's bf16 results are staged in LDS (over the pipeline buffers, free now) and written out as whole
+      // rows: each 16-byte store then covers 8 consecutive channels of one row, where the lanes' own results would
+      // give 16 rows x 8 bytes per instruction. Rows are stored with their 16-byte chunks XOR-swizzled by row, so
+      // both the 8-byte stage writes (16 rows, one column) and the row reads are free of bank conflicts.
+      constexpr int OC = EPI == EPI_GLU ? BN / 2 : BN;  // output channels per tile row
+      constexpr int CPR = OC / 8;                       // 16-byte chunks per row
+      static_assert(BM * OC * 2 <= T::PIPE && (CPR & (CPR - 1)) == 0, "epilogue staging");
+      char* so = smem;
+      auto slot = [&](int row, int col) {  // byte offset of output column col (bf16) of tile row row
+        return row * (OC * 2) + ((((col >> 3) ^ row) & (CPR - 1)) << 4) + (col & 7) * 2;
+      };
+      lds_barrier();  // every wave is done reading the pipeline buffers
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        const int m = m0 + tok(i);
-        if (m >= M) continue;
+        const int rl = tok(i);
 #pragma unroll
         for (int j = 0; j < NI; ++j)
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
-            const int n = n0 + chan(j, q);
+            const int c = chan(j, q);
             float v[4];
             dequant(j, i, q, v);
             if constexpr (EPI == EPI_GLU) {
-              // interleaved (a, gate) channel pairs are adjacent in a lane: output column n / 2
-              const uint32_t o = pack_bf2(round_bf(v[0]) * sigmoid_fast(round_bf(v[1])),
-                                          round_bf(v[2]) * sigmoid_fast(round_bf(v[3])));
-              *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n / 2) = o;
+              // interleaved (a, gate) channel pairs are adjacent in a lane: output column c / 2
+              *reinterpret_cast<uint32_t*>(so + slot(rl, c / 2)) =
+                  pack_bf2(round_bf(v[0]) * sigmoid_fast(round_bf(v[1])), round_bf(v[2]) * sigmoid_fast(round_bf(v[3])));
             } else {
-              uint2 o;
-              if constexpr (EPI == EPI_RESID) {
-                const uint2 rv = *reinterpret_cast<const uint2*>(p.R + (int64_t)m * p.ldr + n);
-                o.x = pack_bf2(__builtin_fmaf(p.alpha, round_bf(v[0]), __uint_as_float(rv.x << 16)),
-                               __builtin_fmaf(p.alpha, round_bf(v[1]), __uint_as_float(rv.x & 0xffff0000u)));
-                o.y = pack_bf2(__builtin_fmaf(p.alpha, round_bf(v[2]), __uint_as_float(rv.y << 16)),
-                               __builtin_fmaf(p.alpha, round_bf(v[3]), __uint_as_float(rv.y & 0xffff0000u)));
-              } else {
-                o.x = pack_bf2(v[0], v[1]);
-                o.y = pack_bf2(v[2], v[3]);
-              }
-              *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + n) = o;
+              *reinterpret_cast<uint2*>(so + slot(rl, c)) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
             }
           }
+      }
+      lds_barrier();
+      const int oc0 = EPI == EPI_GLU ? n0 / 2 : n0;
+      for (int idx = tid; idx < BM * CPR; idx += NT) {
+        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl;
+        if (m >= M) continue;
+        uint4 o = *reinterpret_cast<const uint4*>(so + slot(rl, cc * 8));
+        if constexpr (EPI == EPI_RESID) {
+          // out = bf16(alpha * bf16(v) + r); out may be r itself (this thread reads the chunk before writing it)
+          const uint4 rv = *reinterpret_cast<const uint4*>(p.R + (int64_t)m * p.ldr + oc0 + cc * 8);
+          const uint32_t ov[4] = {o.x, o.y, o.z, o.w}, rr[4] = {rv.x, rv.y, rv.z, rv.w};
+          uint32_t res[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            res[k] = pack_bf2(__builtin_fmaf(p.alpha, __uint_as_float(ov[k] << 16), __uint_as_float(rr[k] << 16)),
+                              __builtin_fmaf(p.alpha, __uint_as_float(ov[k] & 0xffff0000u),
+                                             __uint_as_float(rr[k] & 0xffff0000u)));
+          o = make_uint4(res[0], res[1], res[2], res[3]);
+        }
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(p.C) + (int64_t)m * p.ldc + oc0 + cc * 8) = o;
       }
     } else if constexpr (EPI == EPI_SILU_Q8) {
       // u = bf16(silu(bf16(v))), kept (as float bits) in the accumulator registers; the max |u| of each (row,
@@ -571,7 +639,8 @@ void launch_tile(const GemmArgs& p, hipStream_t s) {
 //   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
 //   5 32x128 (1x4, 4)    6 256x256 (2x4, 2 dense / 3 sparse)        7 64x64 (2x2, 4)    8 256x128 (4x2, 3)
 //   9 128x256 (2x4, 3)   10 256x256 (4x2, 2 dense / 3 sparse)   11 256x128 (2x2, 3)   12 128x128 (2x2, 4)
-//   13 128x256 (2x2, 3); tiles 11-13 use the 32x32 matrix instructions, the others 16x16
+//   13 128x256 (2x2, 3)   14 256x256 (2x2, 2 dense / 3 sparse); tiles 11-13 use the 32x32 matrix instructions,
+//   the others 16x16
 struct TileInfo {
   int bm, bn;
   bool grouped_ok;
@@ -579,7 +648,7 @@ struct TileInfo {
 constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
                               {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
                               {256, 128, true}, {128, 256, true},  {256, 256, false}, {256, 128, false},
-                              {128, 128, true}, {128, 256, false}};
+                              {128, 128, true}, {128, 256, false}, {256, 256, false}};
 constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
 
 // launches tile `tile` for one (SPARSE, EPI, GROUPED); false when the tile has no such instantiation
@@ -604,6 +673,7 @@ bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
       case 10: launch_tile<256, 256, 4, 2, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
       case 11: launch_tile<256, 128, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
       case 13: launch_tile<128, 256, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
+      case 14: launch_tile<256, 256, 2, 2, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
       default: break;
     }
   }
