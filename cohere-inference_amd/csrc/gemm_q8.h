@@ -422,23 +422,31 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     for (int g = 1; g < G; ++g) group(g, std::true_type{});
   } else if constexpr (T::PF) {
     // fragments of step u + 1 are read while the matrix cores work on step u
+    // the steady state has no conditional fragment loads (they made the compiler copy fragment registers at every
+    // join); the last one or two steps are peeled
     Frags F0, F1;
     load_frags(F0, 0);
-    for (int u = 0; u < NSTEPS; u += 2) {
-      if (u + 1 < NSTEPS) {
-        if ((u + 1) % SPS == 0) enter_stage((u + 1) / SPS);
-        load_frags(F1, u + 1);
-      }
+    int u = 0;
+    for (; u + 2 < NSTEPS; u += 2) {
+      if ((u + 1) % SPS == 0) enter_stage((u + 1) / SPS);
+      load_frags(F1, u + 1);
       mma(F0);
       flush_issue();
-      if (u + 1 < NSTEPS) {
-        if (u + 2 < NSTEPS) {
-          if ((u + 2) % SPS == 0) enter_stage((u + 2) / SPS);
-          load_frags(F0, u + 2);
-        }
-        mma(F1);
-        flush_issue();
-      }
+      if ((u + 2) % SPS == 0) enter_stage((u + 2) / SPS);
+      load_frags(F0, u + 2);
+      mma(F1);
+      flush_issue();
+    }
+    if (u + 1 < NSTEPS) {
+      if ((u + 1) % SPS == 0) enter_stage((u + 1) / SPS);
+      load_frags(F1, u + 1);
+      mma(F0);
+      flush_issue();
+      mma(F1);
+      flush_issue();
+    } else {
+      mma(F0);
+      flush_issue();
     }
   } else {
     // two waves per SIMD hide each other's LDS latency
