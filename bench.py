@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block", "decstep"], default=None,
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block", "decstep", "e2e"], default=None,
                     help="run one part only (for rocprofv3 runs)")
     ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
     return ap.parse_args()
@@ -366,6 +366,123 @@ def decoder_step_extra(dev, steps=448):
             "frac_of_hbm": round((weights + kv) / (ms * 1e-3) / PEAK_HBM, 4)}
 
 
+def synthetic_audio(lengths, seed: int = 0):
+    """Config 4's audio: per piece, seeded pink noise (1/f power by FFT shaping) plus random 100-3000 Hz tone bursts
+    (one per second of audio), scaled to -20 dBFS RMS; fp32 numpy arrays."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    out = []
+    for n in lengths:
+        spec = np.fft.rfft(rng.standard_normal(n))
+        f = np.arange(len(spec), dtype=np.float64)
+        f[0] = 1.0
+        pink = np.fft.irfft(spec / np.sqrt(f), n)
+        x = 0.5 * pink / (np.sqrt(np.mean(pink ** 2)) + 1e-12)
+        for _ in range(max(1, n // 16000)):
+            start, dur = int(rng.integers(0, max(1, n - 1))), int(rng.integers(1600, 8000))
+            t = np.arange(min(dur, n - start)) / 16000
+            x[start:start + len(t)] += np.sin(2 * np.pi * rng.uniform(100, 3000) * t)
+        x *= 0.1 / (np.sqrt(np.mean(x ** 2)) + 1e-12)
+        out.append(x.astype(np.float32))
+    return out
+
+
+def random_asr_model(dev, enc_layers: int = 24, seed: int = 1):
+    """Config 4's model: transformers CohereAsrForConditionalGeneration with a 24-block config-2 encoder (d 1280, 16
+    heads, FFN 5120, conv kernel 9, 256 subsampling channels, no input scaling) and config 3's decoder (8 layers, d
+    1024, 8 heads, FFN 4096, vocab 16384), built on the GPU: encoder and projection Xavier-uniform (seeded), decoder
+    and head N(0, 0.05), small random biases / LayerNorm affines / content and position biases / BatchNorm
+    statistics; bf16."""
+    import torch
+    from transformers.models.cohere_asr.configuration_cohere_asr import CohereAsrConfig
+    from transformers.models.cohere_asr.modeling_cohere_asr import CohereAsrForConditionalGeneration
+
+    enc_cfg = {"model_type": "parakeet_encoder", "hidden_size": D, "num_hidden_layers": enc_layers,
+               "num_attention_heads": 16, "num_key_value_heads": 16, "intermediate_size": F, "conv_kernel_size": 9,
+               "subsampling_conv_channels": 256, "num_mel_bins": 128, "subsampling_factor": 8, "scale_input": False,
+               "dropout": 0.0, "attention_dropout": 0.0, "activation_dropout": 0.0, "dropout_positions": 0.0,
+               "layerdrop": 0.0}
+    cfg = CohereAsrConfig(encoder_config=enc_cfg)
+    with torch.device(dev):
+        model = CohereAsrForConditionalGeneration(cfg).eval()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            enc = ".encoder." in name or "decoder.proj." in name
+            if name.endswith(("bias_u", "bias_v")):
+                p.copy_(torch.randn(p.shape, generator=g, device=dev) * 0.2)
+            elif "norm" in name:
+                p.copy_((1.0 if name.endswith("weight") else 0.0) + 0.1 * torch.randn(p.shape, generator=g, device=dev))
+            elif p.dim() >= 2 and enc:
+                torch.nn.init.xavier_uniform_(p, generator=g)
+            else:
+                p.copy_(0.05 * torch.randn(p.shape, generator=g, device=dev))
+        for blk in model.model.encoder.layers:
+            bn = blk.conv.norm
+            bn.running_mean.copy_(0.05 * torch.randn(bn.running_mean.shape, generator=g, device=dev))
+            bn.running_var.copy_(1.0 + 0.2 * torch.rand(bn.running_var.shape, generator=g, device=dev))
+    return model.to(torch.bfloat16)
+
+
+def e2e_extra(dev, clips: int = 32, seconds: float = 30.0, runs: int = 2):
+    """Config 4: 32 clips of 30 s synthetic audio (seeded pink noise + 100-3000 Hz tone bursts at -20 dBFS, dithered
+    as the extractor does) through the whole pipeline -- GPU log-mel, subsampling stem, 24 int8 encoder blocks (2:4
+    feed-forward W2s), projection and cross-attention fill, greedy decoding of up to 448 tokens with continuous
+    batching -- from samples resident on the GPU to token ids. audio-sec/sec = audio seconds / wall seconds of one
+    transcribe() call (after a warm-up call)."""
+    import numpy as np
+    import torch
+
+    from kernels.features import dither
+    from kernels.pipeline import Pipeline
+
+    t0 = time.perf_counter()
+    model = random_asr_model(dev)
+    pipe = Pipeline(model, slots=clips, max_new_tokens=448, int8=True, sparse=True,
+                    buckets=(1, 2, 4, 8, 16, 24, 32))
+    setup_s = time.perf_counter() - t0
+    n = int(seconds * 16000)
+    pieces = [torch.from_numpy(dither(x)).to(dev) for x in synthetic_audio([n] * clips, seed=7)]
+    prompt = torch.tensor([4, 5, 6, 7])
+    pipe.transcribe(pieces, prompt)  # warm-up
+    torch.cuda.synchronize()
+    walls, steps = [], 0
+    for _ in range(runs):
+        s0 = dict(pipe.stats)
+        t = time.perf_counter()
+        tokens = pipe.transcribe(pieces, prompt)
+        torch.cuda.synchronize()
+        walls.append(time.perf_counter() - t)
+        steps = pipe.stats["steps"] - s0["steps"]
+    wall = min(walls)
+    gen = [len(t) - len(prompt) for t in tokens]
+    # stage times of one more call: features, encoder (stem + 24 blocks), cross fill, decode
+    stage = {}
+    feats_ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    with torch.no_grad():
+        feats_ev[0].record()
+        feats, frames = pipe.features(pieces)
+        feats_ev[1].record()
+        hidden, lengths = pipe.encoder(feats, frames)
+        feats_ev[2].record()
+        pipe.decoder.fill_cross(hidden, lengths, list(range(clips)))
+        feats_ev[3].record()
+    torch.cuda.synchronize()
+    stage["features_ms"] = round(feats_ev[0].elapsed_time(feats_ev[1]), 3)
+    stage["encoder_ms"] = round(feats_ev[1].elapsed_time(feats_ev[2]), 3)
+    stage["cross_fill_ms"] = round(feats_ev[2].elapsed_time(feats_ev[3]), 3)
+    audio_s = clips * seconds
+    return {"what": f"config 4: {clips} x {seconds:.0f} s synthetic audio -> log-mel -> stem + 24 int8 blocks -> "
+                    "greedy decode (config-3 decoder, up to 448 tokens), one transcribe() call, samples resident "
+                    "on the GPU",
+            "audio_sec_per_sec": round(audio_s / wall, 1), "wall_s": round(wall, 4),
+            "walls_s": [round(w, 4) for w in walls], "decode_steps": steps,
+            "ms_per_decode_step_upper_bound": round((wall * 1e3 - sum(stage.values())) / max(steps, 1), 4),
+            "generated_tokens_mean": float(np.mean(gen)), "encoder_frames": int(sum(lengths)),
+            "stages": stage, "setup_s": round(setup_s, 1)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -465,6 +582,8 @@ def main():
         result["encoder_block"] = block_extra(dev)
     if not args.no_extras and args.only in (None, "decstep"):
         result["decoder_step"] = decoder_step_extra(dev)
+    if not args.no_extras and args.only in (None, "e2e"):
+        result["e2e_config4"] = e2e_extra(dev)
 
     if args.only is not None:
         print(json.dumps(result))
@@ -485,7 +604,7 @@ def main():
         "kernels_ms": result["kernels_ms"],
     }
     line["frac_of_sparse_peak"] = round(line["value"] * 1e12 / PEAK_INT8_SPARSE, 4)
-    for k in ("dense_config0", "decoder_gemms", "encoder_block", "decoder_step"):
+    for k in ("dense_config0", "decoder_gemms", "encoder_block", "decoder_step", "e2e_config4"):
         if k in result:
             line[k] = result[k]
     if not args.no_cpu:

@@ -41,7 +41,9 @@
 
 namespace cohere_gemm {
 
-enum { EPI_BIAS = 0, EPI_RESID = 3, EPI_GLU = 4, EPI_SILU_Q8 = 5, EPI_I32 = 7 };
+// the reference's epilogue ids (kernels/cuda_ext.py:28); SILU, RELU and CONV_RELU are bf16-operand only, I32 is ours
+enum { EPI_BIAS = 0, EPI_SILU = 1, EPI_RELU = 2, EPI_RESID = 3, EPI_GLU = 4, EPI_SILU_Q8 = 5, EPI_CONV_RELU = 6,
+       EPI_I32 = 7 };
 
 struct GemmArgs {
   const int8_t* X;       // tokens [M, K], row stride ldx
@@ -134,13 +136,23 @@ DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
 // GS > 0 (grouped only): the K steps per scale group, fixed at compile time -- the main loop then runs whole groups
 // with the fold at a static place; GS == 0 reads it from p.group
-template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE, int GS = 0>
+//
+// BF (bf16 operands, kernels/csrc/gemm.cu of the reference): X and W hold bf16 values and K, ldx count bytes (two per
+// value). v_mfma_f32_16x16x32_bf16 / 32x32x16_bf16 take 16 bytes per lane in exactly the lane layout of the int8
+// instructions of the same shape, so the DMA ring, swizzle and fragment reads are shared; accumulation is fp32 and
+// the epilogue adds the bias in fp32 before its first rounding (CONV_RELU rounds the sum first, as a convolution
+// whose bias is added after).
+template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE, int GS = 0,
+          bool BF = false>
 __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) {
+  static_assert(!BF || (!SPARSE && !GROUPED && EPI != EPI_SILU_Q8 && EPI != EPI_I32), "bf16 operands");
+  static_assert(BF || (EPI != EPI_SILU && EPI != EPI_RELU && EPI != EPI_CONV_RELU), "bf16-only epilogue");
   using T = Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>;
   constexpr int NW = T::NW, NT = T::NT, TM = T::TM, TN = T::TN, MI = T::MI, NI = T::NI, LPS = T::LPS;
   constexpr int KSTEP = T::KSTEP, SPS = T::SPS, RPL = T::RPL;
-  using Acc = typename std::conditional<MS == 16, v4i, v16i>::type;
+  using AccI = typename std::conditional<MS == 16, v4i, v16i>::type;
   using AccF = typename std::conditional<MS == 16, v4f, v16f>::type;
+  using Acc = typename std::conditional<BF, AccF, AccI>::type;
   __shared__ __attribute__((aligned(16))) char smem[T::SMEM];
 
   const int M = p.M, N = p.N, K = p.K;
@@ -183,13 +195,13 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 #pragma unroll
       for (int x = 0; x < NPM; ++x) {
         const int i = tid + x * NT;
-        if (!GROUPED && i < BM) psx[x] = p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
+        if (!GROUPED && !BF && i < BM) psx[x] = p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
       }
 #pragma unroll
       for (int x = 0; x < NPN; ++x) {
         const int i = tid + x * NT;
         if (i < BN) {
-          psw[x] = p.sw[n0 + i];
+          psw[x] = BF ? 1.f : p.sw[n0 + i];
           if (p.bias) pbb[x] = p.bias[n0 + i];
         }
       }
@@ -199,7 +211,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     if constexpr (EPI != EPI_I32) {
 #pragma unroll
       for (int x = 0; x < NPM; ++x)
-        if (tid + x * NT < BM) pS[tid + x * NT] = GROUPED ? 1.f : psx[x];
+        if (tid + x * NT < BM) pS[tid + x * NT] = GROUPED || BF ? 1.f : psx[x];
 #pragma unroll
       for (int x = 0; x < NPN; ++x)
         if (tid + x * NT < BN) {
@@ -324,7 +336,13 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   };
   int kstep = 0;
   auto mma_block = [&](const Frags& F, int j, int i) {
-    if constexpr (SPARSE && MS == 16)
+    if constexpr (BF && MS == 16)
+      acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, F.aw[j]),
+                                                         __builtin_bit_cast(v8bf, F.bx[i]), acc[j][i], 0, 0, 0);
+    else if constexpr (BF)
+      acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, F.aw[j]),
+                                                         __builtin_bit_cast(v8bf, F.bx[i]), acc[j][i], 0, 0, 0);
+    else if constexpr (SPARSE && MS == 16)
       acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
     else if constexpr (SPARSE)
       acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
@@ -495,11 +513,17 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       const v4f b4 = *reinterpret_cast<const v4f*>(pB + chan(j, q));
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float x = GROUPED ? accf[j][i][4 * q + r] : (float)acc[j][i][4 * q + r] * srow[i];
-        v[r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
+        if constexpr (BF) {
+          const float x = EPI == EPI_CONV_RELU ? round_bf(acc[j][i][4 * q + r]) : acc[j][i][4 * q + r];
+          v[r] = has_bias ? x + b4[r] : x;
+        } else {
+          const float x = GROUPED ? accf[j][i][4 * q + r] : (float)acc[j][i][4 * q + r] * srow[i];
+          v[r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
+        }
       }
     };
-    if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID || EPI == EPI_GLU) {
+    if constexpr (EPI == EPI_BIAS || EPI == EPI_RESID || EPI == EPI_GLU || EPI == EPI_SILU || EPI == EPI_RELU ||
+                  EPI == EPI_CONV_RELU) {
       // the tile's bf16 results are staged in LDS (over the pipeline buffers, free now) and written out as whole
       // rows: each 16-byte store then covers 8 consecutive channels of one row, where the lanes' own results would
       // give 16 rows x 8 bytes per instruction. Rows are stored with their 16-byte chunks XOR-swizzled by row, so
@@ -527,6 +551,16 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
               *reinterpret_cast<uint32_t*>(so + slot(rl, c / 2)) =
                   pack_bf2(round_bf(v[0]) * sigmoid_fast(round_bf(v[1])), round_bf(v[2]) * sigmoid_fast(round_bf(v[3])));
             } else {
+              if constexpr (EPI == EPI_SILU) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float t = round_bf(v[r]);
+                  v[r] = t * sigmoid_fast(t);
+                }
+              } else if constexpr (EPI == EPI_RELU || EPI == EPI_CONV_RELU) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[r] = fmaxf(v[r], 0.f);
+              }
               *reinterpret_cast<uint2*>(so + slot(rl, c)) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
             }
           }
@@ -628,7 +662,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   }
 }
 
-template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE>
+template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE, bool BF = false>
 void launch_tile(const GemmArgs& p, hipStream_t s) {
   const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
   // the feed-forward W2's grouping (256 K per scale) runs the static-group loop (tiles of one wave per SIMD: with
@@ -640,7 +674,7 @@ void launch_tile(const GemmArgs& p, hipStream_t s) {
       return;
     }
   }
-  gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE><<<grid, WM * WN * 64, 0, s>>>(p);
+  gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE, 0, BF><<<grid, WM * WN * 64, 0, s>>>(p);
 }
 
 // tile ids (tokens x channels, waves M x N, pipeline stages):
@@ -691,5 +725,9 @@ bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
 // instantiated in gemm_q8_dense.hip / gemm_q8_sparse.hip
 template <bool SPARSE>
 bool launch_gemm(int tile, int epi, bool grouped, const GemmArgs& p, hipStream_t s);
+
+// bf16 operands (instantiated in gemm_bf16.hip): the tiles with a bf16 instantiation, and the launch
+constexpr bool bf16_tile(int tile) { return tile == 0 || tile == 1 || tile == 3 || tile == 6 || tile == 7 || tile == 9; }
+bool launch_gemm_bf16(int tile, int epi, const GemmArgs& p, hipStream_t s);
 
 }  // namespace cohere_gemm

@@ -24,9 +24,10 @@ int num_cus() {
   return n;
 }
 
-int choose_tile(const GemmArgs& p, bool grouped) {
+int choose_tile(const GemmArgs& p, bool grouped, bool bf = false) {
   auto fits = [&](int id) {
     const TileInfo& t = TILES[id];
+    if (bf && !bf16_tile(id)) return false;
     if (p.N % t.bn) return false;
     if (grouped && !t.grouped_ok) return false;
     if (p.epi == EPI_SILU_Q8 && t.bn % p.qgroup) return false;
@@ -128,4 +129,37 @@ extern "C" int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int
   p.ldx = ldx; p.ldsx = ldsx; p.ldc = ldc; p.ldr = ldr; p.ldqs = ldqs;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.qgroup = 256; p.epi = epi; p.alpha = alpha;
   return gemm_entry<true>(p, group, 128, reinterpret_cast<hipStream_t>(stream), "gemm_sp");
+}
+
+extern "C" int cohere_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* w, const uint16_t* bias, uint16_t* out,
+                                int64_t ldc, int32_t epi, const uint16_t* resid, int64_t ldr, float alpha, int64_t M,
+                                int64_t N, int64_t K, int32_t cfg, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(cfg == 3 || cfg == 5 || cfg == 8, "gemm: unknown config " + std::to_string(cfg));
+  COHERE_REQUIRE(M >= 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 30),
+                 "gemm: bad sizes");
+  COHERE_REQUIRE(a && w && out, "gemm: null pointer");
+  COHERE_REQUIRE(K % 32 == 0, "gemm: K must match and be a multiple of 32");
+  COHERE_REQUIRE(N % 64 == 0, "gemm: N must be a multiple of 64");
+  COHERE_REQUIRE(epi == EPI_BIAS || epi == EPI_SILU || epi == EPI_RELU || epi == EPI_RESID || epi == EPI_GLU ||
+                     epi == EPI_CONV_RELU,
+                 "gemm: unknown epilogue " + std::to_string(epi));
+  COHERE_REQUIRE(epi != EPI_RESID || resid, "gemm: residual epilogue needs resid");
+  COHERE_REQUIRE(lda % 8 == 0 && aligned16(a) && aligned16(w), "gemm: operand rows must be 16-byte aligned");
+  COHERE_REQUIRE(!bias || (reinterpret_cast<uintptr_t>(bias) & 7) == 0, "gemm: bias must be 8-byte aligned");
+  COHERE_REQUIRE(aligned16(out) && ldc % 8 == 0, "gemm: output rows must be 16-byte aligned");
+  COHERE_REQUIRE(epi != EPI_RESID || (aligned16(resid) && ldr % 8 == 0), "gemm: residual rows must be aligned");
+  if (M == 0) return 0;
+  GemmArgs p{};
+  // the int8 kernel's byte addressing: K and the row stride in bytes
+  p.X = reinterpret_cast<const int8_t*>(a); p.W = reinterpret_cast<const int8_t*>(w); p.bias = bias; p.C = out;
+  p.R = resid; p.ldx = 2 * lda; p.ldc = ldc; p.ldr = ldr;
+  p.M = (int)M; p.N = (int)N; p.K = (int)(2 * K); p.group = p.K; p.qgroup = 256; p.epi = epi; p.alpha = alpha;
+  const int tile = choose_tile(p, false, true);
+  COHERE_REQUIRE(tile >= 0, "gemm: no gfx950 tile fits N=" + std::to_string(p.N));
+  if (!launch_gemm_bf16(tile, epi, p, reinterpret_cast<hipStream_t>(stream))) {
+    cohere::set_error("gemm: tile " + std::to_string(tile) + " has no bf16 kernel for this epilogue");
+    return 1;
+  }
+  return cohere::check_launch("gemm");
 }

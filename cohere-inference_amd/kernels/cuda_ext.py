@@ -32,7 +32,8 @@ EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_l
            "cohere_set_skinny_shape", "cohere_layernorm", "cohere_dwconv_bn_silu", "cohere_dwconv_bn_silu_q8",
            "cohere_relpos_attention", "cohere_encoder_workspace_bytes", "cohere_encoder_layers", "cohere_dec_embed",
            "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
-           "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8")
+           "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8", "cohere_gemm_bf16", "cohere_logmel_workspace_bytes",
+           "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -61,6 +62,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_dec_pick": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P],
         "cohere_dec_scatter_kv": [P, I64, P, P, P, P, I64, I64, I64, I64, P],
         "cohere_dec_scatter_kv_q8": [P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P],
+        "cohere_gemm_bf16": [P, I64, P, P, P, I64, I32, P, I64, F, I64, I64, I64, I32, P],
+        "cohere_logmel_features": [P, P, I64, I64, P, P, P, F, P, I64, P, P],
+        "cohere_sub_conv0_dw": [P, I64, P, P, I64, P, P, P, P, P, I64, P],
+        "cohere_sub_dw": [P, P, P, P, I64, P, P, P, I64, I64, P],
         "cohere_encoder_layers": [P, I64, P, I64, P, P, I64, P, P, I64, I64, I64, ctypes.c_double, I32, I32, I32, P,
                                   I64, P, I64, P],
     }
@@ -70,6 +75,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     lib.cohere_encoder_workspace_bytes.argtypes = [I64, I64]
     lib.cohere_encoder_workspace_bytes.restype = I64
+    lib.cohere_logmel_workspace_bytes.argtypes = [I64]
+    lib.cohere_logmel_workspace_bytes.restype = I64
     lib.cohere_last_error.restype = ctypes.c_char_p
     lib.cohere_last_error.argtypes = []
     lib.cohere_version.restype = ctypes.c_char_p
@@ -112,6 +119,72 @@ class _Ext:
     def set_skinny_shape(self, strips: int, waves: int) -> None:
         """Tuning hook: force the skinny projections' workgroup shape (strips <= 0 = automatic)."""
         self._lib.cohere_set_skinny_shape(int(strips), int(waves))
+
+    # ---- bf16 GEMM (bindings.cpp:3-4, 65) ----------------------------------------------------------------------------
+
+    def gemm(self, a, w, bias, out, epi, resid, alpha, cfg):
+        """out = epilogue(a @ w^T + bias) in bf16 with fp32 accumulation; a (M, K) unit stride along K, w (N, K)
+        contiguous, out (M, N) or (M, N/2) for EPI_GLU (reference kernels/csrc/gemm.cu:246-279)."""
+        _check(a.dtype == torch.bfloat16 and w.dtype == torch.bfloat16, "gemm: bf16 only")
+        _check(a.dim() == 2 and w.dim() == 2 and a.stride(1) == 1 and w.is_contiguous() and out.stride(1) == 1,
+               "gemm: a, out need unit column stride and w must be contiguous")
+        _check(a.shape[1] == w.shape[1] and a.shape[1] % 32 == 0, "gemm: K must match and be a multiple of 32")
+        _check(out.dtype == torch.bfloat16 and (bias is None or bias.dtype == torch.bfloat16), "gemm: bf16 only")
+        _check(epi != EPI_RESID or (resid is not None and resid.stride(1) == 1), "gemm: residual epilogue needs resid")
+        M, K = a.shape
+        if M == 0:
+            return
+        self._call("cohere_gemm_bf16", _ptr(a), a.stride(0), _ptr(w), _ptr(bias), _ptr(out), out.stride(0), int(epi),
+                   _ptr(resid), resid.stride(0) if resid is not None else 0, float(alpha), M, w.shape[0], K, int(cfg),
+                   _stream())
+
+    # ---- front end: log-mel features and the subsampling convolutions (bindings.cpp:51-53, 71-72, 79) ---------------
+
+    def logmel_features(self, x, meta, total_frames, window, mel, band, preemph, out):
+        """Normalized log-mel of packed pieces into out (pieces, T, 128) bf16 (reference kernels/csrc/features.cu:
+        105-132): x fp32 samples back to back; meta int64 (3 pieces + 1); window (512); mel (128, 257); band (128, 2)
+        int32. Frames past each piece's valid frames are left as they are."""
+        _check(x.is_contiguous() and x.dtype == torch.float32 and window.numel() == 512 and band.is_contiguous() and
+               band.numel() == 256 and band.dtype == torch.int32 and mel.shape == (128, 257) and mel.is_contiguous()
+               and out.is_contiguous() and out.dim() == 3 and out.shape[2] == 128 and out.dtype == torch.bfloat16 and
+               meta.dtype == torch.int64 and meta.numel() == 3 * out.shape[0] + 1 and meta.is_contiguous() and
+               window.is_contiguous() and window.dtype == torch.float32 and mel.dtype == torch.float32,
+               "logmel_features: bad arguments")
+        total_frames = int(total_frames)
+        if total_frames == 0:
+            return
+        work = torch.empty(self._lib.cohere_logmel_workspace_bytes(total_frames) // 4, dtype=torch.float32,
+                           device=x.device)
+        self._call("cohere_logmel_features", _ptr(x), _ptr(meta), out.shape[0], total_frames, _ptr(window), _ptr(mel),
+                   _ptr(band), float(preemph), _ptr(out), out.shape[1], _ptr(work), _stream())
+
+    def sub_conv0_dw(self, feats, mel_len, rows, w0, b0, w2, b2, out):
+        """Subsampling conv0 + ReLU + depthwise, per sequence, channels-last: feats (B, T, 128) bf16, mel_len (B)
+        int32, rows (n, 2) int32 (sequence, t2), weights fp32 (C, 9) / (C), out (n, 32, C) bf16 (reference
+        kernels/csrc/encoder_ops.cu:709-719)."""
+        _check(feats.is_contiguous() and feats.dim() == 3 and feats.shape[2] == 128 and out.is_contiguous() and
+               feats.dtype == torch.bfloat16 and out.dtype == torch.bfloat16 and w0.shape[0] == 256 and
+               rows.dtype == torch.int32 and rows.is_contiguous() and mel_len.dtype == torch.int32 and
+               all(t.dtype == torch.float32 and t.is_contiguous() for t in (w0, b0, w2, b2)),
+               "sub_conv0_dw: bad arguments")
+        n = rows.shape[0]
+        if n == 0:
+            return
+        self._call("cohere_sub_conv0_dw", _ptr(feats), feats.stride(0), _ptr(mel_len), _ptr(rows), n, _ptr(w0),
+                   _ptr(b0), _ptr(w2), _ptr(b2), _ptr(out), w0.shape[0], _stream())
+
+    def sub_dw(self, x, in_start, in_len, rows, w, b, out):
+        """Depthwise 3x3 stride-2 + bias on channels-last sequences: x (sum T_in, F_in, C) bf16, in_start / in_len
+        (B) int32, rows (n, 2) int32, out (n, F_in / 2, C) (reference kernels/csrc/encoder_ops.cu:723-734)."""
+        n, F_in, C = rows.shape[0], x.shape[1], x.shape[2]
+        _check(x.is_contiguous() and out.is_contiguous() and C % 8 == 0 and x.dtype == torch.bfloat16 and
+               out.dtype == torch.bfloat16 and rows.dtype == torch.int32 and in_start.dtype == torch.int32 and
+               in_len.dtype == torch.int32 and w.dtype == torch.float32 and b.dtype == torch.float32 and
+               w.is_contiguous(), "sub_dw: bad arguments")
+        if n == 0:
+            return
+        self._call("cohere_sub_dw", _ptr(x), _ptr(in_start), _ptr(in_len), _ptr(rows), n, _ptr(w), _ptr(b),
+                   _ptr(out), F_in, C, _stream())
 
     # ---- int8 GEMMs (bindings.cpp:41-43, 59-61) ----------------------------------------------------------------------
 

@@ -9,13 +9,16 @@ kernels of cohere-inference_amd/csrc (int8 GEMMs, attention, depthwise convoluti
 
     layers = EncoderLayers(hf_blocks, inv_freq, sparse=True)  # transformers ParakeetEncoderBlock modules, bf16 on GPU
     x = layers(x, lengths)                               # packed frames (sum(lengths), 1280) bf16, in place
+
+    enc = FastEncoder(hf_encoder, int8=True, sparse=True)  # subsampling stem + layers (reference FastEncoder)
+    hidden, lengths = enc(features, frames)              # log-mel (B, T, 128) -> packed (sum(lengths), 1280)
 """
 
 from __future__ import annotations
 
 import torch
 
-from kernels.cuda_ext import EPI_BIAS, EPI_GLU, EPI_RESID, EPI_SILU_Q8, ext
+from kernels.cuda_ext import EPI_BIAS, EPI_CONV_RELU, EPI_GLU, EPI_RESID, EPI_SILU_Q8, ext
 from kernels.sparse import compress_24, prune_24_magnitude
 
 # The reference's int8 config ids (A10 tile choices). They are accepted and checked by the gfx950 GEMMs (each id keeps
@@ -43,6 +46,15 @@ def quantize_rows(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     wf = w.float()
     s = wf.abs().amax(-1).clamp_min(1e-12) / 127
     return torch.round(wf / s[:, None]).clamp(-127, 127).to(torch.int8).contiguous(), s.contiguous()
+
+
+def gemm(a, w, b, epi=EPI_BIAS, out=None, resid=None, alpha=1.0, cfg=None):
+    """bf16 out = epilogue(a @ w^T + b) (reference fast_encoder.py:66-71), allocating out when not given."""
+    n = w.shape[0] // 2 if epi == EPI_GLU else w.shape[0]
+    if out is None:
+        out = torch.empty(a.shape[0], n, device=a.device, dtype=a.dtype)
+    ext.gemm(a, w, b, out, epi, resid, alpha, GEMM_CFG if cfg is None else cfg)
+    return out
 
 
 def quantize_activations(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -209,5 +221,87 @@ class EncoderLayers:
         return x
 
 
-__all__ = ["EncoderLayer", "EncoderLayers", "LAYER_FIELDS", "metadata", "relative_table", "EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
+class FastEncoder:
+    """A transformers ParakeetEncoder (bf16, on the GPU) on packed pieces (reference fast_encoder.py:133-232): the
+    subsampling stem per piece without padding (sub_conv0_dw, the pointwise convolutions and final linear as bf16
+    GEMMs, sub_dw), then the int8 layer loop. int8 must be true (the reference's bf16 layer branch is not provided).
+    sparse: a file of 2:4-pruned second feed-forward weights (as the reference), or True to prune them by magnitude
+    here; None keeps every layer dense."""
+
+    MAX_LEN = MAX_LEN
+
+    def __init__(self, encoder, int8: bool = True, sparse: str | bool | None = None):
+        if not int8:
+            raise ValueError("FastEncoder: only the int8 layers are provided")
+        cfg = encoder.config
+        if cfg.hidden_size != 1280 or getattr(cfg, "scale_input", False):
+            raise ValueError("FastEncoder: 1280-wide encoders without input scaling only")
+        if isinstance(sparse, str):
+            pruned = torch.load(sparse, weights_only=True)
+            with torch.no_grad():
+                for key, w in pruned.items():
+                    i, name = key.split(".")
+                    lin = getattr(encoder.layers[int(i)], name).linear2
+                    if w.shape != lin.weight.shape:
+                        raise ValueError(f"FastEncoder: {key} has shape {tuple(w.shape)}")
+                    lin.weight.copy_(w.to(lin.weight.device, lin.weight.dtype))
+            if len(pruned) != 2 * len(encoder.layers):
+                raise ValueError("FastEncoder: the file must prune every feed-forward's second layer")
+        self.encoder, self.int8, self.sparse = encoder, int8, sparse is not None and sparse is not False
+        self.layers = EncoderLayers(encoder.layers, encoder.encode_positions.inv_freq, sparse=self.sparse,
+                                    max_len=self.MAX_LEN)
+        with torch.no_grad():
+            # subsampling: [conv0, ReLU, dw, pw, ReLU, dw, pw, ReLU] + linear; the linear's input columns reordered
+            # from (channel, frequency) to the channels-last (frequency, channel)
+            sub = encoder.subsampling
+            conv0, dw2, pw3, dw5, pw6 = (sub.layers[i] for i in (0, 2, 3, 5, 6))
+            f32 = lambda t: t.float().reshape(t.shape[0], -1).contiguous()  # noqa: E731
+            self.sub_c0 = (f32(conv0.weight), conv0.bias.float().contiguous(), f32(dw2.weight),
+                           dw2.bias.float().contiguous())
+            self.sub_pw3 = (pw3.weight[:, :, 0, 0].contiguous(), pw3.bias.contiguous())
+            self.sub_dw5 = (f32(dw5.weight), dw5.bias.float().contiguous())
+            self.sub_pw6 = (pw6.weight[:, :, 0, 0].contiguous(), pw6.bias.contiguous())
+            ch, out_f = pw6.out_channels, sub.linear.in_features // pw6.out_channels
+            self.sub_lin = (sub.linear.weight.view(-1, ch, out_f).transpose(1, 2).reshape(-1, ch * out_f).contiguous(),
+                            sub.linear.bias.contiguous())
+        self.channels = ch
+
+    @torch.no_grad()
+    def subsample(self, features: torch.Tensor, frames: list[int]) -> tuple[torch.Tensor, list[int]]:
+        """Each piece's first frames[i] log-mel frames of the padded batch features (B, T, 128) through the
+        subsampling convolutions, on its own (no padding), channels-last: packed (N, 1280) and the lengths."""
+        dev, C = features.device, self.channels
+        half = lambda n: [(t - 1) // 2 + 1 for t in n]  # noqa: E731  3x3, stride 2, padding 1
+        t2 = half(half(frames))
+        t3 = half(t2)
+        rows = lambda ts: torch.tensor([(i, t) for i, n in enumerate(ts) for t in range(n)],  # noqa: E731
+                                       dtype=torch.int32).reshape(-1, 2).to(dev, non_blocking=True)
+        i32 = lambda v: torch.tensor(v, dtype=torch.int32).to(dev, non_blocking=True)  # noqa: E731
+        n2, n3 = sum(t2), sum(t3)
+        a2 = torch.empty(n2, 32, C, device=dev, dtype=features.dtype)
+        ext.sub_conv0_dw(features.contiguous(), i32(frames), rows(t2), *self.sub_c0, a2)
+        a3 = gemm(a2.view(n2 * 32, C), *self.sub_pw3, EPI_CONV_RELU)
+        a5 = torch.empty(n3, 16, C, device=dev, dtype=features.dtype)
+        starts = [sum(t2[:i]) for i in range(len(t2))]
+        ext.sub_dw(a3.view(n2, 32, C), i32(starts), i32(t2), rows(t3), *self.sub_dw5, a5)
+        a6 = gemm(a5.view(n3 * 16, C), *self.sub_pw6, EPI_CONV_RELU)
+        return gemm(a6.view(n3, 16 * C), *self.sub_lin, EPI_BIAS), t3
+
+    def metadata(self, lengths: list[int], device) -> dict:
+        return metadata(lengths, device)
+
+    @torch.no_grad()
+    def layers_forward(self, x: torch.Tensor, meta: dict) -> torch.Tensor:
+        """Every layer on packed frames x (N, 1280), in place (the native loop); returns x."""
+        return self.layers(x, None, meta)
+
+    @torch.no_grad()
+    def __call__(self, features: torch.Tensor, frames: list[int]) -> tuple[torch.Tensor, list[int]]:
+        """Packed hidden states (sum of lengths, 1280) and the lengths of the pieces whose first frames[i] frames are
+        in the padded batch features (B, T, 128)."""
+        x, lengths = self.subsample(features, frames)
+        return self.layers_forward(x, self.metadata(lengths, x.device)), lengths
+
+
+__all__ = ["EncoderLayer", "FastEncoder", "gemm", "EncoderLayers", "LAYER_FIELDS", "metadata", "relative_table", "EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
            "I8_SMALL", "SP_CONFIGS", "Int8Linear", "i8_config", "quantize_activations", "quantize_rows"]

@@ -61,6 +61,17 @@ int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, 
                    const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N,
                    int64_t K, int32_t cfg, void* stream);
 
+/* Replaces gemm (reference kernels/csrc/gemm.cu:246-279, bound at kernels/csrc/bindings.cpp:65): bf16
+ * out = epi(a w^T + bias), a bf16 [M, K] (lda), w bf16 [N, K] contiguous, fp32 accumulation, bias bf16 [N] or
+ * null added in fp32 before the first rounding. epi: EPI_BIAS, EPI_SILU (silu(bf16(v))), EPI_RELU, EPI_RESID
+ * (bf16(alpha * bf16(v) + resid), resid may be out), EPI_GLU (interleaved value/gate rows, out [M, N/2]),
+ * EPI_CONV_RELU (relu(bf16(acc) + bias): a convolution whose bias is added after its rounding). Requirements:
+ * K % 32 == 0, N % 64 == 0, 16-byte aligned rows. cfg: the reference's config id (3, 5 or 8), validated, otherwise
+ * ignored (the gfx950 tile is chosen by shape). */
+int cohere_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* w, const uint16_t* bias, uint16_t* out,
+                     int64_t ldc, int32_t epi, const uint16_t* resid, int64_t ldr, float alpha, int64_t M, int64_t N,
+                     int64_t K, int32_t cfg, void* stream);
+
 /* Replaces quantize_rows (reference kernels/csrc/encoder_ops.cu:545-553, bound at bindings.cpp:69): bf16 rows x
  * [rows, cols] (ldx) -> int8 q [rows, cols] (ldq) and fp32 s [rows]; one scale per row, absmax / 127;
  * cols % 8 == 0, cols <= 8192. */
@@ -201,6 +212,41 @@ int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, 
                           int64_t max_len, int64_t rel_rows, double scale, int32_t heads, int32_t head_dim,
                           int32_t int8, const int64_t* cfg, int64_t n_cfg, void* workspace, int64_t workspace_bytes,
                           void* stream);
+
+/* Bytes of device workspace cohere_logmel_features needs for total_frames frames (fp32 log-mel values). */
+int64_t cohere_logmel_workspace_bytes(int64_t total_frames);
+
+/* Replaces logmel_features (reference kernels/csrc/features.cu:105-132, bound at kernels/csrc/bindings.cpp:79;
+ * caller kernels/features.py:76-88): normalized log-mel features of packed pieces, valid frames only. x fp32: the
+ * pieces' (dithered) samples back to back; meta int64 [3 pieces + 1]: each piece's first sample, its length, then
+ * the cumulative valid-frame counts (a piece of n samples has n / 160 valid frames); window fp32 [512] the Hann
+ * window of 400 centred in 512; mel fp32 [128, 257] the filter bank; band int32 [128, 2] each band's first and end
+ * nonzero bin; preemph the pre-emphasis coefficient. out bf16 [pieces, T, 128]: frame t < valid of piece p gets
+ * (log(mel(|rfft|^2) + 2^-24) - mean) / (std + 1e-5) per band over the piece's valid frames (unbiased variance);
+ * other frames are left as they are (the caller zeroes out). work: cohere_logmel_workspace_bytes(total_frames) bytes
+ * of device memory. */
+int cohere_logmel_features(const float* x, const int64_t* meta, int64_t pieces, int64_t total_frames,
+                           const float* window, const float* mel, const int32_t* band, float preemph, uint16_t* out,
+                           int64_t T, float* work, void* stream);
+
+/* Replaces sub_conv0_dw (reference kernels/csrc/encoder_ops.cu:709-719, bound at kernels/csrc/bindings.cpp:71;
+ * caller kernels/fast_encoder.py:196): the subsampling's conv0 (1 -> C, 3x3, stride 2, padding 1) + bias + ReLU and
+ * the first depthwise 3x3 stride-2 convolution + bias, per sequence (zero padding at its ends), channels-last.
+ * feats bf16 [B, T, 128] (ld_seq elements between sequences); mel_len int32 [B] frames per sequence; rows int32
+ * [n_rows, 2] (sequence, output row t2); w0 / w2 fp32 [C, 9], b0 / b2 fp32 [C]; out bf16 [n_rows, 32, C].
+ * C % 64 == 0, C <= 1024. */
+int cohere_sub_conv0_dw(const uint16_t* feats, int64_t ld_seq, const int32_t* mel_len, const int32_t* rows,
+                        int64_t n_rows, const float* w0, const float* b0, const float* w2, const float* b2,
+                        uint16_t* out, int64_t C, void* stream);
+
+/* Replaces sub_dw (reference kernels/csrc/encoder_ops.cu:723-734, bound at kernels/csrc/bindings.cpp:72; caller
+ * kernels/fast_encoder.py:199): depthwise 3x3 stride-2 convolution + bias on channels-last sequences. x bf16
+ * [sum T_in, F_in, C] with in_start / in_len int32 [B] each sequence's first row and row count; rows int32
+ * [n_rows, 2] (sequence, output row); w fp32 [C, 9], b fp32 [C]; out bf16 [n_rows, F_in / 2, C]. C % 8 == 0,
+ * 16-byte aligned x and out. */
+int cohere_sub_dw(const uint16_t* x, const int32_t* in_start, const int32_t* in_len, const int32_t* rows,
+                  int64_t n_rows, const float* w, const float* b, uint16_t* out, int64_t F_in, int64_t C,
+                  void* stream);
 
 /* The last error on this thread ("" when none). */
 const char* cohere_last_error(void);

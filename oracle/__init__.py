@@ -91,6 +91,11 @@ def lib() -> ctypes.CDLL:
         _lib.orc_prepare_w8.argtypes = [p, i64, i64, p, p]
         _lib.orc_dec_w8_linear.argtypes = [p, i64, p, p, p, p, i64, ctypes.c_int, i64, i64, i64, ctypes.c_int]
         _lib.orc_linear_bf16.argtypes = [p, i64, p, p, p, i64, ctypes.c_int, i64, i64, i64, ctypes.c_int]
+        _lib.orc_gemm_bf16.argtypes = [p, i64, p, p, p, i64, ctypes.c_int, p, i64, ctypes.c_float, i64, i64, i64,
+                                       ctypes.c_int]
+        _lib.orc_logmel.argtypes = [p, p, i64, p, p, p, ctypes.c_float, p, i64, ctypes.c_int]
+        _lib.orc_sub_conv0_dw.argtypes = [p, i64, p, p, i64, p, p, p, p, p, i64, ctypes.c_int]
+        _lib.orc_sub_dw.argtypes = [p, p, p, p, i64, p, p, p, i64, i64, ctypes.c_int]
         _lib.orc_f32_to_bf16.argtypes = [p, p, i64]
         _lib.orc_bf16_to_f32.argtypes = [p, p, i64]
     return _lib
@@ -433,3 +438,64 @@ def decoder_step(W, st, b, int8=True):
     dec_pick(logits, act, st["dummy"], st["tok"], st["pos"], st["finished"], st["forced"], st["plen"], st["limit"],
              st["out"], W["eos"])
     return logits
+
+
+# ---- bf16 GEMM and the encoder's front end (config 4) -----------------------------------------------------------
+
+def gemm_bf16(a, w, bias, epi, resid=None, alpha=1.0, threads=0):
+    """gemm.cu:150-212: bf16 bits a [M, K] @ w [N, K]^T with the epilogue -> bf16 bits [M, N] ([M, N/2] for GLU)."""
+    a, w = _c(a, np.uint16), _c(w, np.uint16)
+    M, K = a.shape
+    N = w.shape[0]
+    bias = None if bias is None else _c(bias, np.uint16)
+    out = np.empty((M, N // 2 if epi == EPI_GLU else N), np.uint16)
+    r = _c(resid, np.uint16) if epi == EPI_RESID else None
+    lib().orc_gemm_bf16(_p(a), K, _p(w), _p(bias), _p(out), out.shape[1], epi, _p(r), N if r is not None else 0,
+                        alpha, M, N, K, threads)
+    return out
+
+
+def logmel_meta(lengths) -> np.ndarray:
+    """meta int64 [3 pieces + 1] of pieces with these sample counts (first sample, length, cumulative valid frames)."""
+    lengths = np.asarray(lengths, np.int64)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]])
+    valid = lengths // 160
+    return np.concatenate([starts, lengths, np.concatenate([[0], np.cumsum(valid)])]).astype(np.int64)
+
+
+def logmel(x, lengths, window, mel, band, preemph, T=None, threads=0):
+    """features.cu:34-102: normalized log-mel of the pieces (fp32 samples back to back) -> bf16 bits
+    [pieces, T, 128], zero past each piece's valid frames (T defaults to max(n // 160) + 1)."""
+    x = _c(x, np.float32)
+    meta = logmel_meta(lengths)
+    pieces = len(lengths)
+    if T is None:
+        T = max(n // 160 for n in lengths) + 1
+    out = np.zeros((pieces, T, 128), np.uint16)
+    lib().orc_logmel(_p(x), _p(meta), pieces, _p(_c(window, np.float32)), _p(_c(mel, np.float32)),
+                     _p(_c(band, np.int32)), preemph, _p(out), T, threads)
+    return out
+
+
+def sub_conv0_dw(feats, mel_len, rows, w0, b0, w2, b2, threads=0):
+    """encoder_ops.cu:339-413: feats bf16 bits [B, T, 128]; rows int32 [n, 2] (sequence, t2) -> bf16 bits
+    [n, 32, C]."""
+    feats = _c(feats, np.uint16)
+    rows = _c(rows, np.int32).reshape(-1, 2)
+    C = w0.shape[0]
+    out = np.empty((rows.shape[0], 32, C), np.uint16)
+    lib().orc_sub_conv0_dw(_p(feats), feats.shape[1] * 128, _p(_c(mel_len, np.int32)), _p(rows), rows.shape[0],
+                           _p(_c(w0, np.float32)), _p(_c(b0, np.float32)), _p(_c(w2, np.float32)),
+                           _p(_c(b2, np.float32)), _p(out), C, threads)
+    return out
+
+
+def sub_dw(x, in_start, in_len, rows, w, b, threads=0):
+    """encoder_ops.cu:415-448: x bf16 bits [sum T_in, F_in, C] -> bf16 bits [n, F_in / 2, C]."""
+    x = _c(x, np.uint16)
+    _, F_in, C = x.shape
+    rows = _c(rows, np.int32).reshape(-1, 2)
+    out = np.empty((rows.shape[0], F_in // 2, C), np.uint16)
+    lib().orc_sub_dw(_p(x), _p(_c(in_start, np.int32)), _p(_c(in_len, np.int32)), _p(rows), rows.shape[0],
+                     _p(_c(w, np.float32)), _p(_c(b, np.float32)), _p(out), F_in, C, threads)
+    return out

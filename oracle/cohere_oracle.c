@@ -571,6 +571,205 @@ void orc_dec_scatter_kv(int q8, const uint16_t* kv, int64_t rows, const int32_t*
         }
 }
 
+/* ---- bf16 GEMM and the encoder's front end (config 4) ----------------------------------------------------------- */
+
+/* kernels/csrc/gemm.cu:150-212: out = epi(a W^T + bias) on bf16 operands. The accumulator (fp32 in the kernel, here
+ * fp64 rounded to fp32 once), then in fp32: CONV_RELU rounds it to bf16 first; + bias; BIAS -> bf16; SILU t = bf16(v),
+ * t * sigmoid(t); RELU / CONV_RELU max(v, 0); GLU bf16(bf16(v[2j]) * sigmoid(bf16(v[2j+1]))); RESID
+ * bf16(fmaf(alpha, bf16(v), r)) (r may be out). */
+void orc_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* w, const uint16_t* bias, uint16_t* out,
+                   int64_t ldc, int epi, const uint16_t* resid, int64_t ldr, float alpha, int64_t M, int64_t N,
+                   int64_t K, int nthreads) {
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t m = 0; m < M; ++m) {
+    float* v = (float*)malloc(sizeof(float) * N);
+    for (int64_t n = 0; n < N; ++n) {
+      double acc = 0.0;
+      for (int64_t k = 0; k < K; ++k) acc += (double)bf2f(a[m * lda + k]) * (double)bf2f(w[n * K + k]);
+      float x = (float)acc;
+      if (epi == 6) x = round_bf(x);
+      if (bias) x = x + bf2f(bias[n]);
+      v[n] = x;
+    }
+    uint16_t* o = out + m * ldc;
+    if (epi == 4) {
+      for (int64_t j = 0; j < N / 2; ++j) o[j] = f2bf(round_bf(v[2 * j]) * sigmoid(round_bf(v[2 * j + 1])));
+    } else {
+      for (int64_t n = 0; n < N; ++n) {
+        float x = v[n];
+        if (epi == 1) {
+          const float t = round_bf(x);
+          x = t * sigmoid(t);
+        } else if (epi == 2 || epi == 6) {
+          x = fmaxf(x, 0.f);
+        } else if (epi == 3) {
+          x = fmaf(alpha, round_bf(x), bf2f(resid[m * ldr + n]));
+        }
+        o[n] = f2bf(x);
+      }
+    }
+    free(v);
+  }
+}
+
+/* in-place radix-2 FFT of n (a power of two) complex doubles, forward (e^{-2 pi i k n / N}) */
+static void fft_double(double* re, double* im, int n) {
+  for (int i = 1, j = 0; i < n; ++i) {
+    int bit = n >> 1;
+    for (; j & bit; bit >>= 1) j ^= bit;
+    j ^= bit;
+    if (i < j) {
+      double t = re[i]; re[i] = re[j]; re[j] = t;
+      t = im[i]; im[i] = im[j]; im[j] = t;
+    }
+  }
+  for (int len = 2; len <= n; len <<= 1) {
+    for (int i = 0; i < n; i += len)
+      for (int k = 0; k < len / 2; ++k) {
+        const double ang = -2.0 * 3.14159265358979323846 * k / len, c = cos(ang), s = sin(ang);
+        const double xr = re[i + k + len / 2], xi = im[i + k + len / 2];
+        const double tr = xr * c - xi * s, ti = xr * s + xi * c;
+        re[i + k + len / 2] = re[i + k] - tr;
+        im[i + k + len / 2] = im[i + k] - ti;
+        re[i + k] += tr;
+        im[i + k] += ti;
+      }
+  }
+}
+
+/* kernels/csrc/features.cu:34-102 (and kernels/features.py:90-108, transformers' CohereAsrFeatureExtractor): for each
+ * valid frame t < n / 160 of each piece, the 512 samples centred at 160 t, pre-emphasised (x[s] - fp32(p x[s-1])),
+ * zero outside the piece, times the window (fp32); the real DFT (here in fp64, rounded to fp32); power
+ * fp32(sqrt(re^2 + im^2))^2; mel bands as fp32 fma over their nonzero bins in order; log(mel + 2^-24); then per piece
+ * and band (v - mean) / (std + 1e-5) with fp64 mean and unbiased variance, bf16 into out [pieces, T, 128] (other
+ * frames untouched). meta as cohere_logmel_features: first sample, length, cumulative valid frames. */
+void orc_logmel(const float* x, const int64_t* meta, int64_t pieces, const float* window, const float* mel,
+                const int32_t* band, float preemph, uint16_t* out, int64_t T, int nthreads) {
+  enum { NF = 512, NB = 257, NM = 128 };
+  set_threads(nthreads);
+  const int64_t* frame_start = meta + 2 * pieces;
+  const int64_t total = frame_start[pieces];
+  float* lm = (float*)malloc(sizeof(float) * (total > 0 ? total : 1) * NM);
+#pragma omp parallel for schedule(dynamic, 16)
+  for (int64_t f = 0; f < total; ++f) {
+    int64_t p = 0;
+    while (p + 1 < pieces && frame_start[p + 1] <= f) ++p;
+    const int64_t t = f - frame_start[p], n = meta[pieces + p];
+    const float* xp = x + meta[p];
+    double re[NF], im[NF];
+    for (int j = 0; j < NF; ++j) {
+      const int64_t s = t * 160 - NF / 2 + j;
+      float e = 0.f;
+      if (s >= 0 && s < n) e = s == 0 ? xp[0] : xp[s] - preemph * xp[s - 1];
+      re[j] = (double)(e * window[j]);
+      im[j] = 0.0;
+    }
+    fft_double(re, im, NF);
+    float pw[NB];
+    for (int k = 0; k < NB; ++k) {
+      const float r = (float)re[k], i = (float)im[k];
+      const float a = sqrtf(r * r + i * i);
+      pw[k] = a * a;
+    }
+    for (int m = 0; m < NM; ++m) {
+      float acc = 0.f;
+      for (int k = band[2 * m]; k < band[2 * m + 1]; ++k) acc = fmaf(mel[m * NB + k], pw[k], acc);
+      lm[f * NM + m] = logf(acc + 5.9604644775390625e-8f);
+    }
+  }
+#pragma omp parallel for schedule(static)
+  for (int64_t p = 0; p < pieces; ++p) {
+    const int64_t f0 = frame_start[p], nv = frame_start[p + 1] - f0;
+    if (nv == 0) continue;
+    for (int m = 0; m < NM; ++m) {
+      double s = 0.0;
+      for (int64_t t = 0; t < nv; ++t) s += lm[(f0 + t) * NM + m];
+      const float mean = (float)(s / (double)nv);
+      double q = 0.0;
+      for (int64_t t = 0; t < nv; ++t) {
+        const double d = (double)lm[(f0 + t) * NM + m] - (double)mean;
+        q += d * d;
+      }
+      const float den = (float)sqrt(q / (double)(nv - 1)) + 1e-5f;
+      for (int64_t t = 0; t < nv; ++t) out[(p * T + t) * NM + m] = f2bf((lm[(f0 + t) * NM + m] - mean) / den);
+    }
+  }
+  free(lm);
+}
+
+/* kernels/csrc/encoder_ops.cu:339-413 (transformers' ParakeetEncoderSubsamplingConv2D layers 0-2 per sequence):
+ * conv0 (1 -> C, 3x3, stride 2, padding 1) as an fp32 fma chain over its taps row by row from 0, rounded to bf16, +
+ * bias, rounded again, ReLU; then the depthwise 3x3 stride-2 convolution from its bias, an fp32 fma per tap row by
+ * row, one rounding. Rows of conv0 / the mel input outside the sequence are zeros. out [n_rows, 32, C]. */
+void orc_sub_conv0_dw(const uint16_t* feats, int64_t ld_seq, const int32_t* mel_len, const int32_t* rows,
+                      int64_t n_rows, const float* w0, const float* b0, const float* w2, const float* b2, uint16_t* out,
+                      int64_t C, int nthreads) {
+  enum { NM = 128, F1 = 64, F2 = 32 };
+  set_threads(nthreads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n_rows; ++i) {
+    const int seq = rows[2 * i], t2 = rows[2 * i + 1], L = mel_len[seq], T1 = (L - 1) / 2 + 1;
+    const uint16_t* xs = feats + seq * ld_seq;
+    for (int64_t c = 0; c < C; ++c) {
+      float c0[3][F1];  /* conv0 rows 2 t2 - 1 .. 2 t2 + 1, after ReLU; zero outside */
+      for (int r = 0; r < 3; ++r) {
+        const int t1 = 2 * t2 - 1 + r;
+        for (int f1 = 0; f1 < F1; ++f1) {
+          if (t1 < 0 || t1 >= T1) { c0[r][f1] = 0.f; continue; }
+          float s = 0.f;
+          for (int di = 0; di < 3; ++di)
+            for (int dj = 0; dj < 3; ++dj) {
+              const int mr = 2 * t1 - 1 + di, mc = 2 * f1 - 1 + dj;
+              const float v = (mr >= 0 && mr < L && mc >= 0 && mc < NM) ? bf2f(xs[(int64_t)mr * NM + mc]) : 0.f;
+              s = fmaf(w0[c * 9 + di * 3 + dj], v, s);
+            }
+          c0[r][f1] = fmaxf(round_bf(round_bf(s) + b0[c]), 0.f);
+        }
+      }
+      for (int f2 = 0; f2 < F2; ++f2) {
+        float acc = b2[c];
+        for (int r = 0; r < 3; ++r) {
+          if (2 * t2 - 1 + r < 0 || 2 * t2 - 1 + r >= T1) continue;
+          for (int dj = 0; dj < 3; ++dj) {
+            const int f1 = 2 * f2 - 1 + dj;
+            if (f1 < 0 || f1 >= F1) continue;
+            acc = fmaf(w2[c * 9 + r * 3 + dj], c0[r][f1], acc);
+          }
+        }
+        out[(i * F2 + f2) * C + c] = f2bf(acc);
+      }
+    }
+  }
+}
+
+/* kernels/csrc/encoder_ops.cu:415-448: depthwise 3x3 stride-2 convolution + bias on channels-last sequences x
+ * [sum T_in, F_in, C] (in_start / in_len per sequence), from the bias, an fp32 fma per tap row by row, one rounding:
+ * out [n_rows, F_in / 2, C] for rows (sequence, t). */
+void orc_sub_dw(const uint16_t* x, const int32_t* in_start, const int32_t* in_len, const int32_t* rows, int64_t n_rows,
+                const float* w, const float* b, uint16_t* out, int64_t F_in, int64_t C, int nthreads) {
+  set_threads(nthreads);
+  const int64_t F_out = F_in / 2;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n_rows; ++i) {
+    const int seq = rows[2 * i], t = rows[2 * i + 1], start = in_start[seq], len = in_len[seq];
+    for (int64_t f = 0; f < F_out; ++f)
+      for (int64_t c = 0; c < C; ++c) {
+        float acc = b[c];
+        for (int di = 0; di < 3; ++di) {
+          const int ti = 2 * t - 1 + di;
+          if (ti < 0 || ti >= len) continue;
+          for (int dj = 0; dj < 3; ++dj) {
+            const int64_t fi = 2 * f - 1 + dj;
+            if (fi < 0 || fi >= F_in) continue;
+            acc = fmaf(w[c * 9 + di * 3 + dj], bf2f(x[(((int64_t)start + ti) * F_in + fi) * C + c]), acc);
+          }
+        }
+        out[(i * F_out + f) * C + c] = f2bf(acc);
+      }
+  }
+}
+
 /* bf16 <-> fp32 helpers exported for the Python side of the checker */
 void orc_f32_to_bf16(const float* f, uint16_t* h, int64_t n) {
   for (int64_t i = 0; i < n; ++i) h[i] = f2bf(f[i]);
