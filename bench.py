@@ -487,7 +487,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards by data "
-              "parallelism with no exchange (see DESIGN.md), and no multi-GPU figure is produced.", file=sys.stderr)
+              "parallelism with no exchange, and no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
     import torch
 

@@ -38,6 +38,14 @@ Function -> reference -> what pins it (tests/test_oracle.py unless noted):
                                                         slot with its own cache) on the dequantized weights
   encoder_layers_int8   kernels/csrc/encoder_loop.cpp:63-99  transformers' ParakeetEncoderBlock in float32 on the
                                                         dequantized weights (within the int8 activation error)
+  gemm_bf16             kernels/csrc/gemm.cu:150-212     exact small-integer operands: numpy int64 matmul and each
+                                                        epilogue's closed form (tests/test_frontend_oracle.py)
+  logmel                kernels/csrc/features.cu:34-102  transformers' CohereAsrFeatureExtractor.__call__ (torch.stft,
+                                                        its normalization) on the same dithered pieces, the Slaney
+                                                        filter bank pinned against transformers.audio_utils
+  sub_conv0_dw, sub_dw  kernels/csrc/encoder_ops.cu:339-448  torch conv2d in float64 (with conv0's two roundings);
+                                                        the whole stem against transformers'
+                                                        ParakeetEncoderSubsamplingConv2D in float32
 """
 
 from __future__ import annotations
