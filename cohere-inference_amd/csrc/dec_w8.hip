@@ -182,6 +182,7 @@ int launch_shape(int ns, int nw, const SkinnyArgs& p, hipStream_t s) {
     case (1 << 8) | 8: launch_rows<1, 8, W8, RELU>(p, s); break;
     case (1 << 8) | 4: launch_rows<1, 4, W8, RELU>(p, s); break;
     case (2 << 8) | 8: launch_rows<2, 8, W8, RELU>(p, s); break;
+    case (2 << 8) | 4: launch_rows<2, 4, W8, RELU>(p, s); break;
     case (4 << 8) | 8: launch_rows<4, 8, W8, RELU>(p, s); break;
     case (4 << 8) | 4: launch_rows<4, 4, W8, RELU>(p, s); break;
     default: cohere::set_error("skinny: no kernel for ns=" + std::to_string(ns) + " nw=" + std::to_string(nw));
@@ -190,16 +191,21 @@ int launch_shape(int ns, int nw, const SkinnyArgs& p, hipStream_t s) {
   return 0;
 }
 
-// channels per workgroup and waves per workgroup: enough workgroups for the CUs, at least one K block per wave
-void choose_shape(int N, int K, int& ns, int& nw) {
+// channels per workgroup (strips of 16) and waves per workgroup, measured on MI355X for the decoder's shapes (graph
+// replays, 1-64 rows): 8 waves; one strip while the workgroups of one strip per 16 rows stay at or below ~256, more
+// strips per workgroup beyond that (2 for 17-32 rows, 4 above, for N of 2048-8192; the head, N >= 8192, keeps 2
+// strips and whole row blocks up to 32 rows). Long K (the feed-forward's second projection) keeps one strip.
+void choose_shape(int N, int K, int M, int& ns, int& nw) {
   if (g_skinny_override > 0) {
     ns = g_skinny_override >> 8;
     nw = g_skinny_override & 255;
     if (N % (ns * 16) == 0) return;
   }
-  ns = N / 16 >= 2048 ? 4 : (N / 16 >= 1024 ? 2 : 1);
-  const int nkb = K / KB;
-  nw = ns == 1 ? (nkb >= 16 ? 16 : (nkb >= 8 ? 8 : 4)) : 8;
+  nw = 8;
+  if (K >= 2048 || N < 2048) ns = 1;
+  else if (N >= 8192) ns = M > 32 ? 4 : 2;
+  else ns = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  while (ns > 1 && N % (ns * 16) != 0) ns >>= 1;
 }
 
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
@@ -213,7 +219,7 @@ int skinny_entry(SkinnyArgs& p, bool w8, int relu, hipStream_t s, const char* na
   COHERE_REQUIRE(al16(p.X) && p.ldx % 8 == 0 && al16(p.W), nm + ": x rows and weights must be 16-byte aligned");
   if (p.M == 0) return 0;
   int ns, nw;
-  choose_shape(p.N, p.K, ns, nw);
+  choose_shape(p.N, p.K, p.M, ns, nw);
   int rc;
   if (w8) rc = relu ? launch_shape<true, true>(ns, nw, p, s) : launch_shape<true, false>(ns, nw, p, s);
   else rc = relu ? launch_shape<false, true>(ns, nw, p, s) : launch_shape<false, false>(ns, nw, p, s);

@@ -70,10 +70,11 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
 }
 
 // ---- attention of one new token per row ---------------------------------------------------------------------------
-// A workgroup of 256 threads per (row, head, split): 32 groups of 8 lanes, each lane 16 of the 128 dims, each group
-// taking every 32nd key of the split, 8 (int8) or 4 (bf16) keys per pass with all their loads in flight at once. Per
+// A workgroup of 512 threads per (row, head, split): 64 groups of 8 lanes, each lane 16 of the 128 dims, each group
+// taking every 64th key of the split, 8 (int8) or 4 (bf16) keys per pass with all their loads in flight at once (a
+// whole 448-token self cache or 375-frame cross cache in one memory round trip). Per
 // key the group's partial dot products meet through three lane shuffles; the online softmax runs in fp32 per group,
-// one rescale per pass; the 32 groups are combined through LDS at the end (or, with several splits, written as
+// one rescale per pass; the 64 groups are combined through LDS at the end (or, with several splits, written as
 // partials (o[128], max, sum) for dec_combine).
 struct DecAttnArgs {
   const int32_t* active;
@@ -92,7 +93,7 @@ struct DecAttnArgs {
   float* part;        // (rows, H, splits, 130) when split
 };
 
-constexpr int AG = 32;  // key groups per workgroup (8 lanes each: 256 threads)
+constexpr int AG = 64;  // key groups per workgroup (8 lanes each: 512 threads; one pass covers 512 int8 keys)
 
 DEVI void load16_bf(const uint16_t* p, float (&f)[16]) {
   const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
@@ -184,6 +185,27 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
   float q[16];
   load16_bf(p.q + (int64_t)r * p.ldq + h * HD + gl * 16, q);
   const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
+  constexpr int KB = Q8 ? 8 : 4;
+  uint4 kr[KB][Q8 ? 1 : 2], vr[KB][Q8 ? 1 : 2];
+  float ksc[KB], vsc[KB];
+  auto load_pass = [&](int j0, int limit) {
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int jj = j0 + i * AG;
+      const int64_t vec = vec0 + (jj < limit ? jj : 0);
+      if constexpr (Q8) {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + vec * HD + gl * 16);
+        vr[i][0] = *reinterpret_cast<const uint4*>(p.v8 + vec * HD + gl * 16);
+        ksc[i] = p.ks[vec];
+        vsc[i] = p.vs[vec];
+      } else {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16);
+        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16 + 8);
+        vr[i][0] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16);
+        vr[i][1] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16 + 8);
+      }
+    }
+  };
   const int n = p.n[s];
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
@@ -208,28 +230,11 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
     attend_one(q, kn, vn, p.scale, m, l, acc);
   }
   const int chunk = (n + nsp - 1) / nsp, start = sp * chunk, end = min(n, start + chunk);
-  // each group takes KB keys per pass (every 32nd key), all loads issued before any use: one memory round trip per
-  // KB keys; then one softmax update for the block
-  constexpr int KB = Q8 ? 8 : 4;
-  for (int j0 = start + grp; j0 < end; j0 += KB * AG) {
-    uint4 kr[KB][Q8 ? 1 : 2], vr[KB][Q8 ? 1 : 2];
-    float ksc[KB], vsc[KB];
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      const int jj = j0 + i * AG;
-      const int64_t vec = vec0 + (jj < end ? jj : start);
-      if constexpr (Q8) {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + vec * HD + gl * 16);
-        vr[i][0] = *reinterpret_cast<const uint4*>(p.v8 + vec * HD + gl * 16);
-        ksc[i] = p.ks[vec];
-        vsc[i] = p.vs[vec];
-      } else {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16);
-        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16 + 8);
-        vr[i][0] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16);
-        vr[i][1] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16 + 8);
-      }
-    }
+  // each group takes KB keys per pass (every 64th key), all loads issued before any use: one memory round trip per
+  // pass; then one softmax update for the pass
+  int j0 = start + grp;
+  if (j0 < end) load_pass(j0, end);
+  for (; j0 < end; j0 += KB * AG) {
     float sc[KB], mb = m;
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
@@ -260,6 +265,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
       for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(ew, vv[k], acc[k]);
     }
     m = mb;
+    if (j0 + KB * AG < end) load_pass(j0 + KB * AG, end);
   }
   // combine the groups: weights exp(m_g - M)
   if (gl == 0) {
@@ -324,15 +330,27 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
   const uint16_t* row = logits + (int64_t)r * V;
   float best = -INFINITY;
   int arg = 0x7fffffff;
-  for (int i = tid * 8; i < V; i += 256 * 8) {
-    const uint4 u = *reinterpret_cast<const uint4*>(row + i);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  // eight 16-byte loads per thread in flight at once (a 16384-entry row in one memory round trip), then the scan in
+  // index order per thread
+  constexpr int LB = 8;
+  for (int i0 = tid * 8; i0 < V; i0 += 256 * 8 * LB) {
+    uint4 u[LB];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float v = __uint_as_float(k & 1 ? w[k >> 1] & 0xffff0000u : w[k >> 1] << 16);
-      if (v > best) {  // strictly greater: the first index of a tie stays
-        best = v;
-        arg = i + k;
+    for (int j = 0; j < LB; ++j) {
+      const int i = i0 + j * 256 * 8;
+      u[j] = i < V ? *reinterpret_cast<const uint4*>(row + i) : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u,
+                                                                           0xff80ff80u);  // -inf: never picked
+    }
+#pragma unroll
+    for (int j = 0; j < LB; ++j) {
+      const uint32_t w[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float v = __uint_as_float(k & 1 ? w[k >> 1] & 0xffff0000u : w[k >> 1] << 16);
+        if (v > best) {  // strictly greater: the first index of a tie stays
+          best = v;
+          arg = i0 + j * 256 * 8 + k;
+        }
       }
     }
   }
