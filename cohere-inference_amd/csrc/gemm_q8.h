@@ -183,49 +183,43 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   const int group_steps = GS > 0 ? GS : (GROUPED ? p.group / KSTEP : 1);
   const int G = GROUPED ? K / p.group : 1;
   const bool scales_in_lds = GROUPED && G <= T::GMAX;
-  // per-row / per-channel epilogue values: loaded into registers between the first stage's DMA and the others (so
-  // their latency overlaps the transfers), stored to LDS once the first stage has landed
-  // (each kind in its own registers, unconverted: using a loaded value before the first wait would make the compiler
-  // wait for the first stage's transfers too)
-  constexpr int NPM = (BM + NT - 1) / NT, NPN = (BN + NT - 1) / NT;
-  float psx[NPM], psw[NPN];
-  uint16_t pbb[NPN];
-  auto load_params = [&]() {
+  // the epilogue's per-row / per-channel values and (grouped) every group's token scales: copied into LDS by the
+  // load unit itself (global_load_lds, 4 bytes a lane), issued between the first stage's transfers and the others.
+  // They hold no registers and need no wait of their own: the first stage's wait covers them (they are older than
+  // the later stages' transfers), and a value loaded into a register and used before that wait would make the compiler
+  // wait for the first stage's transfers too. The bias stays bf16 in LDS (pairs of values per lane).
+  uint16_t* pBh = reinterpret_cast<uint16_t*>(pB);
+  auto dma4 = [&](const void* g, void* lds) { __builtin_amdgcn_global_load_lds(g, (LDS_AS void*)lds, 4, 0, 0); };
+  auto issue_params = [&]() {
     if constexpr (EPI != EPI_I32) {
+      int k = 0;  // instruction index across the kinds, dealt round-robin to the waves
+      if constexpr (!GROUPED && !BF) {
 #pragma unroll
-      for (int x = 0; x < NPM; ++x) {
-        const int i = tid + x * NT;
-        if (!GROUPED && !BF && i < BM) psx[x] = p.sx[(int64_t)min(m0 + i, M - 1) * p.ldsx];
+        for (int b = 0; b < BM; b += 64, ++k)
+          if (k % NW == wave && b + lane < BM) dma4(p.sx + (int64_t)min(m0 + b + lane, M - 1) * p.ldsx, pS + b);
       }
+      if constexpr (!BF) {
 #pragma unroll
-      for (int x = 0; x < NPN; ++x) {
-        const int i = tid + x * NT;
-        if (i < BN) {
-          psw[x] = BF ? 1.f : p.sw[n0 + i];
-          if (p.bias) pbb[x] = p.bias[n0 + i];
-        }
+        for (int b = 0; b < BN; b += 64, ++k)
+          if (k % NW == wave) dma4(p.sw + n0 + b + lane, pW + b);
+      }
+      if (p.bias) {
+#pragma unroll
+        for (int b = 0; b < BN / 2; b += 64, ++k)
+          if (k % NW == wave && b + lane < BN / 2)
+            dma4(reinterpret_cast<const uint32_t*>(p.bias + n0) + b + lane, pBh + 2 * b);
+      }
+      if constexpr (GROUPED) {
+        // group g's scales of rows r0 .. r0 + 63 to sS[g][r0 ..]
+        if (scales_in_lds)
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int b = 0; b < BM; b += 64, ++k)
+              if (k % NW == wave && b + lane < BM)
+                dma4(p.sx + (int64_t)min(m0 + b + lane, M - 1) * p.ldsx + g, sS + g * BM + b);
       }
     }
   };
-  auto store_params = [&]() {
-    if constexpr (EPI != EPI_I32) {
-#pragma unroll
-      for (int x = 0; x < NPM; ++x)
-        if (tid + x * NT < BM) pS[tid + x * NT] = GROUPED || BF ? 1.f : psx[x];
-#pragma unroll
-      for (int x = 0; x < NPN; ++x)
-        if (tid + x * NT < BN) {
-          pW[tid + x * NT] = psw[x];
-          pB[tid + x * NT] = p.bias ? bf2f(pbb[x]) : 0.f;
-        }
-    }
-  };
-  if (scales_in_lds) {
-    for (int i = tid; i < G * BM; i += NT) {
-      const int g = i / BM, r = i % BM;
-      sS[i] = p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
-    }
-  }
 
   auto issue = [&](int buf, int kt) {
     char* base = smem + buf * T::STAGE;
@@ -405,12 +399,11 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   };
 
   issue(0, 0);
-  load_params();
+  issue_params();
 #pragma unroll
   for (int s = 1; s < ST; ++s)
     if (s < KT) issue(s, s);
   wait_stages<LPS, ST>(min(KT - 1, ST - 1));
-  store_params();
   lds_barrier();
   if constexpr (GS > 0) {
     // whole groups of GS steps, unrolled: the fold sits at each group's first step (not the first group's), so the
@@ -510,7 +503,9 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     const bool has_bias = p.bias != nullptr;
     auto dequant = [&](int j, int i, int q, float (&v)[4]) {
       const v4f w4 = *reinterpret_cast<const v4f*>(pW + chan(j, q));
-      const v4f b4 = *reinterpret_cast<const v4f*>(pB + chan(j, q));
+      const uint2 braw = *reinterpret_cast<const uint2*>(pBh + chan(j, q));
+      const float b4[4] = {__uint_as_float(braw.x << 16), __uint_as_float(braw.x & 0xffff0000u),
+                           __uint_as_float(braw.y << 16), __uint_as_float(braw.y & 0xffff0000u)};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if constexpr (BF) {

@@ -30,13 +30,16 @@ class Pipeline:
     LAG = 1  # steps between a step's launch and the host reading its end flags (reference pipeline.py:64)
 
     def __init__(self, model, extractor=None, slots: int = 128, max_new_tokens: int = 448, int8: bool = True,
-                 sparse: str | bool | None = None, frames: int | None = None, buckets=None):
+                 sparse: str | bool | None = None, frames: int | None = None, buckets=None,
+                 chunk_frames: int | None = None):
         dev = model.proj_out.weight.device
         self.features = Features(extractor, device=dev)
         self.encoder = FastEncoder(model.model.encoder, int8=int8, sparse=sparse)
         self.decoder = StreamDecoder(model, slots=slots, max_new_tokens=max_new_tokens, int8=int8, frames=frames,
                                      buckets=buckets)
         self.stats = {"steps": 0, "chunks": 0, "frames": 0}
+        if chunk_frames is not None:  # encoder frames per call (the reference's 3000 keeps a service's calls short)
+            self.CHUNK_FRAMES = chunk_frames
 
     @staticmethod
     def prepare(samples: np.ndarray) -> np.ndarray:
