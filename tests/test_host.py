@@ -75,6 +75,22 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc != 0 and "workspace" in msg
     rc, msg = _raw(lib, "cohere_quantize_rows", fake, 1284, fake, 1284, fake, 4, 1284, None)
     assert rc != 0 and "multiple of 8" in msg
+    # bf16 GEMM: the reference's config ids, K % 32, N % 64
+    rc, msg = _raw(lib, "cohere_gemm_bf16", fake, 96, fake, None, fake, 64, 0, None, 0, 1.0, 4, 64, 96, 7, None)
+    assert rc != 0 and "unknown config 7" in msg
+    rc, msg = _raw(lib, "cohere_gemm_bf16", fake, 80, fake, None, fake, 64, 0, None, 0, 1.0, 4, 64, 80, 8, None)
+    assert rc != 0 and "multiple of 32" in msg
+    rc, msg = _raw(lib, "cohere_gemm_bf16", fake, 96, fake, None, fake, 48, 0, None, 0, 1.0, 4, 48, 96, 8, None)
+    assert rc != 0 and "N must be" in msg
+    rc, msg = _raw(lib, "cohere_gemm_bf16", fake, 96, fake, None, fake, 64, 5, None, 0, 1.0, 4, 64, 96, 8, None)
+    assert rc != 0 and "unknown epilogue 5" in msg  # SILU_Q8 is int8-only
+    # front end: channel counts, empty batches are no-ops
+    rc, msg = _raw(lib, "cohere_sub_conv0_dw", fake, 1280, fake, fake, 3, fake, fake, fake, fake, fake, 100, None)
+    assert rc != 0 and "multiple of 64" in msg
+    rc, msg = _raw(lib, "cohere_sub_dw", fake, fake, fake, fake, 3, fake, fake, fake, 32, 12, None)
+    assert rc != 0 and "C % 8" in msg
+    assert _raw(lib, "cohere_logmel_features", None, None, 0, 0, None, None, None, 0.97, None, 0, None, None)[0] == 0
+    assert lib.cohere_logmel_workspace_bytes(100) == 100 * 128 * 4
 
 
 def test_ext_raises_runtime_error_like_torch_check():
