@@ -72,6 +72,14 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[s][mb] = v4f{0.f, 0.f, 0.f, 0.f};
+  // the epilogue's channel scale and bias: a thread always writes channel n0 + tid % COLS (COLS divides the thread
+  // count), so both are loaded now, with the weights, not after the reduction (the bias load is unconditional -- from
+  // the weights when there is no bias, the value then unused: a load under a branch is waited for at the join)
+  static_assert((NW * 64) % COLS == 0, "epilogue channel per thread");
+  const int n_ep = n0 + (int)(threadIdx.x % COLS);
+  const float sw_ep = W8 ? p.sw[n_ep] : 1.f;
+  const uint16_t* bsrc = p.bias ? p.bias : static_cast<const uint16_t*>(p.W);
+  const uint16_t b_ep = bsrc[n_ep];
 
   for (int b0 = wave; b0 < nkb; b0 += NW * MAXB) {
     uint4 wreg[MAXB][NS][W8 ? 1 : 2];
@@ -144,14 +152,14 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   __syncthreads();
   const int rows = min(p.M - m_base, MB * 16);
   for (int i = threadIdx.x; i < rows * COLS; i += NW * 64) {
-    const int r = i / COLS, c = i % COLS, n = n0 + c, m = m_base + r;
+    const int r = i / COLS, c = i % COLS, m = m_base + r;
     float v = red[0][r][c];
 #pragma unroll
     for (int w = 1; w < NW; ++w) v += red[w][r][c];
-    if constexpr (W8) v = __builtin_fmaf(v, p.sw[n], p.bias ? bf2f(p.bias[n]) : 0.f);
-    else if (p.bias) v = v + bf2f(p.bias[n]);
+    if constexpr (W8) v = __builtin_fmaf(v, sw_ep, p.bias ? bf2f(b_ep) : 0.f);
+    else if (p.bias) v = v + bf2f(b_ep);
     if (RELU) v = fmaxf(v, 0.f);
-    p.Y[(int64_t)m * p.ldy + n] = f2bf(v);
+    p.Y[(int64_t)m * p.ldy + n0 + c] = f2bf(v);
   }
 }
 

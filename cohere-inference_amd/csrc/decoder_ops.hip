@@ -35,6 +35,7 @@ __global__ void __launch_bounds__(256) dec_embed_kernel(const int32_t* __restric
                                                         uint16_t* h, int rows, int width) {
   const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
   if (row >= rows) return;
+  const LnParams<VEC> p0 = load_ln<VEC>(w0, b0, width, lane), p1 = load_ln<VEC>(w1, b1, width, lane);
   const int s = active[row];
   const int64_t t = tok[s];
   const int p = pos[s];
@@ -45,9 +46,9 @@ __global__ void __launch_bounds__(256) dec_embed_kernel(const int32_t* __restric
   for (int i = 0; i < VEC; ++i)
 #pragma unroll
     for (int k = 0; k < 8; ++k) e.v[i][k] = round_bf(e.v[i][k] + q.v[i][k]);
-  ln_row<VEC>(e, width, lane, w0, b0, eps0);
+  ln_row<VEC>(e, width, lane, p0, eps0);
   store_row<VEC>(e, width, lane, x + (int64_t)row * width);
-  ln_row<VEC>(e, width, lane, w1, b1, eps1);
+  ln_row<VEC>(e, width, lane, p1, eps1);
   store_row<VEC>(e, width, lane, h + (int64_t)row * width);
 }
 
@@ -57,6 +58,7 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
                                                          uint16_t* h, int rows, int width) {
   const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
   if (row >= rows) return;
+  const LnParams<VEC> lp = load_ln<VEC>(w, b, width, lane);
   Row<VEC> a, d;
   load_row<VEC>(x + (int64_t)row * width, width, lane, a);
   load_row<VEC>(y + (int64_t)row * ldy, width, lane, d);
@@ -65,7 +67,7 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
 #pragma unroll
     for (int k = 0; k < 8; ++k) a.v[i][k] = round_bf(a.v[i][k] + d.v[i][k]);
   store_row<VEC>(a, width, lane, x + (int64_t)row * width);
-  ln_row<VEC>(a, width, lane, w, b, eps);
+  ln_row<VEC>(a, width, lane, lp, eps);
   store_row<VEC>(a, width, lane, h + (int64_t)row * width);
 }
 
@@ -206,6 +208,11 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
       }
     }
   };
+  // cross-attention: the first pass is issued before the slot's length is known (clamped to the cache's T frames,
+  // masked by the length after), so the key loads do not wait for it; the frame count is close to T anyway.
+  // Self-attention lengths grow from 1, so there the length is waited for.
+  const bool early = !SELF && nsp == 1;
+  if (early) load_pass(grp, p.T);
   const int n = p.n[s];
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
@@ -233,7 +240,7 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
   // each group takes KB keys per pass (every 64th key), all loads issued before any use: one memory round trip per
   // pass; then one softmax update for the pass
   int j0 = start + grp;
-  if (j0 < end) load_pass(j0, end);
+  if (!early && j0 < end) load_pass(j0, end);
   for (; j0 < end; j0 += KB * AG) {
     float sc[KB], mb = m;
 #pragma unroll
@@ -325,8 +332,7 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
   __shared__ float sb[4];
   __shared__ int sa[4];
   const int r = blockIdx.x, tid = threadIdx.x;
-  const int s = active[r];
-  if (s == dummy) return;
+  const int s = active[r];  // a padding row (the dummy slot) is scanned too and then dropped: its loads do not wait
   const uint16_t* row = logits + (int64_t)r * V;
   float best = -INFINITY;
   int arg = 0x7fffffff;
@@ -367,7 +373,7 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
     sa[tid >> 6] = arg;
   }
   __syncthreads();
-  if (tid != 0) return;
+  if (tid != 0 || s == dummy) return;
   for (int w = 1; w < 4; ++w)
     if (sb[w] > best || (sb[w] == best && sa[w] < arg)) {
       best = sb[w];

@@ -35,13 +35,16 @@ __global__ void __launch_bounds__(256) layernorm_kernel(uint16_t* x, int64_t ldx
                                                         float* hs, uint16_t* h, int64_t ldh, int rows, int cols) {
   const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
   if (row >= rows) return;
+  const LnParams<VEC> p1 = load_ln<VEC>(w1, b1, cols, lane);
+  LnParams<VEC> p2;
+  if constexpr (TWO) p2 = load_ln<VEC>(w2, b2, cols, lane);
   Row<VEC> r;
   uint16_t* xr = x + (int64_t)row * ldx;
   load_row<VEC>(xr, cols, lane, r);
-  ln_row<VEC>(r, cols, lane, w1, b1, eps1);
+  ln_row<VEC>(r, cols, lane, p1, eps1);
   if constexpr (TWO) {
     store_row<VEC>(r, cols, lane, xr);
-    ln_row<VEC>(r, cols, lane, w2, b2, eps2);
+    ln_row<VEC>(r, cols, lane, p2, eps2);
   }
   if constexpr (Q8)
     store_q8<VEC>(r, cols, lane, hq + (int64_t)row * ldq, hs + row);

@@ -56,9 +56,28 @@ DEVI float wave_sum(float v) {
   return v;
 }
 
+// a LayerNorm's weight and bias as this lane's 16-byte chunks (bf16), loaded before the row's statistics so that no
+// load waits behind them
+template <int VEC>
+struct LnParams {
+  uint4 w[VEC], b[VEC];
+};
+
+template <int VEC>
+DEVI LnParams<VEC> load_ln(const uint16_t* w, const uint16_t* b, int cols, int lane) {
+  LnParams<VEC> p;
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    p.w[i] = c < cols ? *reinterpret_cast<const uint4*>(w + c) : make_uint4(0, 0, 0, 0);
+    p.b[i] = c < cols ? *reinterpret_cast<const uint4*>(b + c) : make_uint4(0, 0, 0, 0);
+  }
+  return p;
+}
+
 // LayerNorm of the row in place (fp32 statistics over the bf16 inputs), the result rounded to bf16
 template <int VEC>
-DEVI void ln_row(Row<VEC>& r, int cols, int lane, const uint16_t* w, const uint16_t* b, float eps) {
+DEVI void ln_row(Row<VEC>& r, int cols, int lane, const LnParams<VEC>& p, float eps) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i)
@@ -80,8 +99,7 @@ DEVI void ln_row(Row<VEC>& r, int cols, int lane, const uint16_t* w, const uint1
   for (int i = 0; i < VEC; ++i) {
     const int c = (i * 64 + lane) * 8;
     if (c >= cols) continue;
-    const uint4 wv = *reinterpret_cast<const uint4*>(w + c), bv = *reinterpret_cast<const uint4*>(b + c);
-    const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, bb[4] = {bv.x, bv.y, bv.z, bv.w};
+    const uint32_t ww[4] = {p.w[i].x, p.w[i].y, p.w[i].z, p.w[i].w}, bb[4] = {p.b[i].x, p.b[i].y, p.b[i].z, p.b[i].w};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const float wk = __uint_as_float(k & 1 ? ww[k >> 1] & 0xffff0000u : ww[k >> 1] << 16);
