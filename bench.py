@@ -578,6 +578,18 @@ def main():
         result["dense_config0"] = {"what": "dense W8A8 3000x5120x1280, bias epilogue (config 0)",
                                    "ms": round(ms_d, 5), "TOPS": round(ops_up / (ms_d * 1e-3) / 1e12, 1),
                                    "frac_of_dense_peak": round(ops_up / (ms_d * 1e-3) / PEAK_INT8_DENSE, 4)}
+        # the vendor library on the same shapes, for scale: hipBLASLt through torch._int_mm (int32 out, no scales,
+        # bias or bf16 conversion -- less work than the kernels above)
+        vendor = {}
+        for name, (mm, nn, kk) in (("config0", (M, F, D)), ("down", (M, D, F))):
+            xa = torch.randint(-127, 128, (mm, kk), dtype=torch.int8, device=dev)
+            wa = torch.randint(-127, 128, (nn, kk), dtype=torch.int8, device=dev)
+            ms_v = time_graph(graph_of(lambda: torch._int_mm(xa, wa.t()), 20), 10) / 20
+            vendor[name] = {"shape": [mm, nn, kk], "ms": round(ms_v, 5),
+                            "TOPS": round(2 * mm * nn * kk / (ms_v * 1e-3) / 1e12, 1)}
+            del xa, wa
+        result["dense_config0"]["vendor_int_mm"] = dict(
+            what="hipBLASLt via torch._int_mm, dense int8, int32 output only", **vendor)
     if not args.no_extras and args.only in (None, "decoder"):
         result["decoder_gemms"] = decoder_extra(dev)
 

@@ -92,7 +92,7 @@ struct Tile {
   static_assert(X_SLOTS % NW == 0 && W_SLOTS % NW == 0 && BN / NW <= 64, "DMA slots must split evenly over waves");
   static_assert(LPS * (ST - 1) <= 63 && ST >= 2 && ST <= 4, "vmcnt range");
   static_assert(SMEM <= LDS_BYTES, "LDS");
-  static_assert(BM * (BN / MS + BN / 64) * 4 <= PIPE, "SILU_Q8 row-max tables reuse the pipeline buffers");
+  static_assert(BM * (BN / MS + 2 * BN / 64) * 4 <= PIPE, "SILU_Q8 tables reuse the pipeline buffers");
   static_assert(!GROUPED || GMAX >= 1, "grouped tile needs room for scales");
 };
 
@@ -400,6 +400,12 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 
   issue(0, 0);
   issue_params();
+  if constexpr (EPI != EPI_I32) {
+    // no bias: -0.0 in its place, so the epilogue's one fma (x * w + b, or x + b) equals the plain product (sum)
+    // bit for bit, the sign of a zero included
+    if (!p.bias)
+      for (int c = tid; c < BN / 2; c += NT) reinterpret_cast<uint32_t*>(pBh)[c] = 0x80008000u;
+  }
 #pragma unroll
   for (int s = 1; s < ST; ++s)
     if (s < KT) issue(s, s);
@@ -500,7 +506,6 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     float srow[MI];
 #pragma unroll
     for (int i = 0; i < MI; ++i) srow[i] = pS[tok(i)];
-    const bool has_bias = p.bias != nullptr;
     auto dequant = [&](int j, int i, int q, float (&v)[4]) {
       const v4f w4 = *reinterpret_cast<const v4f*>(pW + chan(j, q));
       const uint2 braw = *reinterpret_cast<const uint2*>(pBh + chan(j, q));
@@ -510,10 +515,10 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       for (int r = 0; r < 4; ++r) {
         if constexpr (BF) {
           const float x = EPI == EPI_CONV_RELU ? round_bf(acc[j][i][4 * q + r]) : acc[j][i][4 * q + r];
-          v[r] = has_bias ? x + b4[r] : x;
+          v[r] = x + b4[r];
         } else {
           const float x = GROUPED ? accf[j][i][4 * q + r] : (float)acc[j][i][4 * q + r] * srow[i];
-          v[r] = has_bias ? __builtin_fmaf(x, w4[r], b4[r]) : x * w4[r];
+          v[r] = __builtin_fmaf(x, w4[r], b4[r]);
         }
       }
     };
@@ -613,9 +618,11 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
           if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
         }
       __syncthreads();
-      // each (row, column group) maximum once, from the block table, into gmax [BM][BN / qgroup]
+      // each (row, column group) maximum once, from the block table, and from it the group's scale and its reciprocal
+      // into gsc / ginv [BM][BN / qgroup]
       const int blocks = p.qgroup / MS, ngroups = BN / p.qgroup;
-      float* gmax = red + BM * CB;
+      float* gsc = red + BM * CB;
+      float* ginv = gsc + BM * (BN / 64);
       for (int id = tid; id < BM * ngroups; id += NT) {
         const float* src = red + (id / ngroups) * CB + (id % ngroups) * blocks;
         float mx = 0.f;
@@ -627,18 +634,28 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
         } else {
           for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, src[b]);
         }
-        gmax[id] = mx;
+        const float sc = mx > 0.f ? mx / 127.f : 1.f;
+        gsc[id] = sc;
+        ginv[id] = 1.f / sc;
       }
       __syncthreads();
+      // the int8 tile is staged in LDS past the tables and written out as whole rows (16-byte stores of 16
+      // consecutive channels, where the lanes' own values would be 4-byte stores, 16 rows per instruction); 16-byte
+      // chunks are XOR-swizzled by row, so the 4-byte stage writes (16 rows, one chunk) and the row reads are free of
+      // bank conflicts
+      constexpr int CPR = BN / 16;  // 16-byte chunks per tile row
+      constexpr int TABLES = BM * (CB + 2 * BN / 64) * 4;
+      static_assert(TABLES + BM * BN <= T::PIPE && (CPR & (CPR - 1)) == 0, "int8 staging");
+      char* so = smem + TABLES;
+      auto slot = [&](int row, int col) { return row * BN + ((((col >> 4) ^ row) & (CPR - 1)) << 4) + (col & 15); };
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int rl = tok(i), m = m0 + rl;
 #pragma unroll
         for (int j = 0; j < NI; ++j) {
           const int cb = (wn * TN + j * MS) / MS, g0 = cb - cb % blocks;
-          const float mx = gmax[rl * ngroups + cb / blocks];
-          const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
-          if (m >= M) continue;
+          const int gi = rl * ngroups + cb / blocks;
+          const float inv = ginv[gi];
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
             uint32_t o = 0;
@@ -648,10 +665,17 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
               const int qi = (int)rintf(fminf(fmaxf(u * inv, -127.f), 127.f));
               o |= (uint32_t)(qi & 0xff) << (8 * r);
             }
-            *reinterpret_cast<uint32_t*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n0 + chan(j, q)) = o;
+            *reinterpret_cast<uint32_t*>(so + slot(rl, chan(j, q))) = o;
           }
-          if (lhi == 0 && cb == g0) p.qs[(int64_t)m * p.ldqs + (n0 + cb * MS) / p.qgroup] = sc;
+          if (lhi == 0 && cb == g0 && m < M) p.qs[(int64_t)m * p.ldqs + (n0 + cb * MS) / p.qgroup] = gsc[gi];
         }
+      }
+      lds_barrier();
+      for (int idx = tid; idx < BM * CPR; idx += NT) {
+        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl;
+        if (m >= M) continue;
+        *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n0 + cc * 16) =
+            *reinterpret_cast<const uint4*>(so + slot(rl, cc * 16));
       }
     }
   }

@@ -81,7 +81,7 @@ int gemm_entry(GemmArgs& p, int64_t group, int64_t lda_k_req, hipStream_t s, con
   COHERE_REQUIRE(aligned16(p.W) && aligned16(p.sw), nm + ": weights must be 16-byte aligned");
   COHERE_REQUIRE(!SPARSE || aligned16(p.E), nm + ": selectors must be 16-byte aligned");
   COHERE_REQUIRE(!p.bias || (reinterpret_cast<uintptr_t>(p.bias) & 7) == 0, nm + ": bias must be 8-byte aligned");
-  const int out_align = p.epi == EPI_SILU_Q8 ? 8 : 16;
+  const int out_align = 16;  // the staged epilogues write 16-byte chunks of output rows
   const int esize = p.epi == EPI_SILU_Q8 ? 1 : (p.epi == EPI_I32 ? 4 : 2);
   COHERE_REQUIRE((reinterpret_cast<uintptr_t>(p.C) % out_align) == 0 && (p.ldc * esize) % out_align == 0,
                  nm + ": output rows must be aligned");
