@@ -179,8 +179,9 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
 
 template <bool SELF, bool Q8>
 __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs p) {
-  __shared__ float sm[AG], sl[AG];
+  __shared__ float sm[AG], sl[AG], sw[AG], sML[2];
   __shared__ float sacc[AG][HD + 4];
+  __shared__ float spart[4][HD];
   const int r = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
   const int s = p.active[r];
   const int tid = threadIdx.x, grp = tid >> 3, gl = tid & 7;
@@ -274,7 +275,8 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
     m = mb;
     if (j0 + KB * AG < end) load_pass(j0 + KB * AG, end);
   }
-  // combine the groups: weights exp(m_g - M)
+  // combine the groups: weights w_g = exp(m_g - M). One wave finds M, the weights and L = sum w_g l_g; then every
+  // thread sums 16 groups of one output dimension, and the four partial sums are added in order.
   if (gl == 0) {
     sm[grp] = m;
     sl[grp] = l;
@@ -282,19 +284,34 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
 #pragma unroll
   for (int k = 0; k < 16; ++k) sacc[grp][gl * 16 + k] = acc[k];
   __syncthreads();
-  if (tid >= HD) return;
-  float M = -INFINITY;
+  static_assert(AG == 64 && AG * 8 == 4 * 128, "one weight per lane of the first wave; four partial sums per dim");
+  if (tid < 64) {
+    const float mg = sm[tid];
+    float M = mg;
 #pragma unroll
-  for (int g = 0; g < AG; ++g) M = fmaxf(M, sm[g]);
-  float L = 0.f, O = 0.f;
-  if (M != -INFINITY) {
-#pragma unroll 8
-    for (int g = 0; g < AG; ++g) {
-      const float w = __expf(sm[g] - M);
-      L = __builtin_fmaf(w, sl[g], L);
-      O = __builtin_fmaf(w, sacc[g][tid], O);
+    for (int o = 1; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    const float w = M == -INFINITY ? 0.f : __expf(mg - M);
+    float L = w * sl[tid];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
+    sw[tid] = w;
+    if (tid == 0) {
+      sML[0] = M;
+      sML[1] = L;
     }
   }
+  __syncthreads();
+  {
+    const int d = tid & (HD - 1), part = tid >> 7;
+    float o = 0.f;
+#pragma unroll
+    for (int g = part * 16; g < part * 16 + 16; ++g) o = __builtin_fmaf(sw[g], sacc[g][d], o);
+    spart[part][d] = o;
+  }
+  __syncthreads();
+  if (tid >= HD) return;
+  const float M = sML[0], L = sML[1];
+  const float O = (spart[0][tid] + spart[1][tid]) + (spart[2][tid] + spart[3][tid]);
   if (nsp == 1) {
     p.out[(int64_t)r * p.H * HD + h * HD + tid] = f2bf(O / L);
   } else {
