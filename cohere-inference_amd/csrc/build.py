@@ -27,7 +27,11 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", f"-I{INCLUDE}", f"-I{CSRC}",
           "-Wall", "-Wno-unused-result"]
-DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-x", "hip"]
+# -amdgpu-mfma-vgpr-form: matrix-instruction accumulators in ordinary VGPRs (gfx950 allows either file), so that
+# the VALU work on them (the grouped GEMM's per-group fold, the attention's softmax rescale) needs no
+# v_accvgpr_read/write copies
+DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-x", "hip"]
 
 
 def _compile(src: str) -> str:
