@@ -269,10 +269,28 @@ __global__ void __launch_bounds__(256) sub_dw_kernel(const uint16_t* __restrict_
   const int c = (int)(id % chunks) * 8, fo = (int)((id / chunks) % F_out);
   const int64_t i = id / chunks / F_out;
   const int seq = rows[2 * i], t = rows[2 * i + 1];
-  const int start = in_start[seq], len = in_len[seq];
-  float acc[8];
+  // this thread's 8 channels x 9 taps are 72 consecutive floats of the (C, 9) layout: 18 16-byte loads, issued
+  // with the bias before the row's own loads (not one 4-byte load per tap inside the guarded loops)
+  float wk[8 * 9], acc[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) acc[k] = b[c + k];
+  for (int v = 0; v < 18; ++v)
+    *reinterpret_cast<float4*>(wk + 4 * v) = *reinterpret_cast<const float4*>(w + (int64_t)c * 9 + 4 * v);
+  *reinterpret_cast<float4*>(acc) = *reinterpret_cast<const float4*>(b + c);
+  *reinterpret_cast<float4*>(acc + 4) = *reinterpret_cast<const float4*>(b + c + 4);
+  const int start = in_start[seq], len = in_len[seq];
+  // the 3 x 3 input chunks (zero outside the sequence or the frequency range), all loaded before the first use
+  uint4 u[9];
+#pragma unroll
+  for (int di = 0; di < 3; ++di)
+#pragma unroll
+    for (int dj = 0; dj < 3; ++dj) {
+      const int ti = 2 * t - 1 + di, fi = 2 * fo - 1 + dj;
+      const bool in = ti >= 0 && ti < len && fi >= 0 && fi < F_in;
+      const int64_t off = in ? (((int64_t)start + ti) * F_in + fi) * C + c : 0;
+      u[di * 3 + dj] = *reinterpret_cast<const uint4*>(x + off);
+      if (!in) u[di * 3 + dj] = make_uint4(0, 0, 0, 0);
+    }
+  // the taps in the same order as before (missing taps skipped, not added as zeros: the fma chain is unchanged)
 #pragma unroll
   for (int di = 0; di < 3; ++di) {
     const int ti = 2 * t - 1 + di;
@@ -281,12 +299,12 @@ __global__ void __launch_bounds__(256) sub_dw_kernel(const uint16_t* __restrict_
     for (int dj = 0; dj < 3; ++dj) {
       const int fi = 2 * fo - 1 + dj;
       if (fi < 0 || fi >= F_in) continue;
-      const uint4 u = *reinterpret_cast<const uint4*>(x + (((int64_t)start + ti) * F_in + fi) * C + c);
-      const uint32_t e[4] = {u.x, u.y, u.z, u.w};
+      const uint4 v = u[di * 3 + dj];
+      const uint32_t e[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const float xv = __uint_as_float(k & 1 ? e[k / 2] & 0xffff0000u : e[k / 2] << 16);
-        acc[k] = __builtin_fmaf(w[(c + k) * 9 + di * 3 + dj], xv, acc[k]);
+        acc[k] = __builtin_fmaf(wk[k * 9 + di * 3 + dj], xv, acc[k]);
       }
     }
   }
@@ -343,7 +361,8 @@ extern "C" int cohere_sub_dw(const uint16_t* x, const int32_t* in_start, const i
                  "sub_dw: bad sizes (C % 8 == 0)");
   if (n_rows == 0) return 0;
   COHERE_REQUIRE(x && in_start && in_len && rows && w && b && out, "sub_dw: null pointer");
-  COHERE_REQUIRE(aligned(x, 16) && aligned(out, 16), "sub_dw: x and out must be 16-byte aligned");
+  COHERE_REQUIRE(aligned(x, 16) && aligned(out, 16) && aligned(w, 16) && aligned(b, 16),
+                 "sub_dw: x, out, the taps and the bias must be 16-byte aligned");
   const int64_t total = n_rows * (F_in / 2) * (C / 8);
   COHERE_REQUIRE((total + 255) / 256 < (1LL << 31), "sub_dw: too many rows");
   sub_dw_kernel<<<(unsigned)((total + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
