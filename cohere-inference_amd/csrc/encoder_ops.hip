@@ -144,14 +144,14 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
 // needs spans 95 distances; each wave computes its own 48 (3 blocks of 16) from a ring of 128 table rows in LDS, of
 // which each key tile adds 32, rounds them as the module does and gathers its scores from them through a small
 // per-wave LDS buffer.
-constexpr int AT_Q = 64, AT_KEYS = 32, AT_RING = 128, AT_PW = 56;  // per-wave position buffer row (48 + pad)
+constexpr int AT_Q = 64, AT_KEYS = 32, AT_RING = 128, AT_PW = 52;  // per-wave position buffer row (48 + pad)
 
 template <int D>
 struct AttnShape {
   static constexpr int DP = D + 8;            // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
   static constexpr int KS = (D + 31) / 32;    // k steps of 32 over the head size (the last one zero-padded)
   static constexpr int OB = D / 16;           // 16-dim blocks of the output
-  static constexpr int VT = AT_KEYS + 8;      // LDS row of the transposed value tile
+  static constexpr int VT = AT_KEYS + 4;      // LDS row of the transposed value tile
   static constexpr int K_ELEMS = AT_KEYS * DP, V_ELEMS = D * VT, R_ELEMS = AT_RING * DP, P_ELEMS = 4 * 16 * AT_PW;
   static constexpr int LDS_BYTES = 2 * (K_ELEMS + V_ELEMS + R_ELEMS + P_ELEMS);
   static_assert(D % 16 == 0, "head size");
@@ -191,7 +191,8 @@ DEVI v8bf q_plus(const uint16_t* qrow, const uint16_t* bias, int col, bool valid
 }
 
 template <int D>
-__global__ void __launch_bounds__(256) relpos_attention_kernel(const AttnArgs p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 80 ? 4 : 1, D == 80 ? 4 : 8)))
+relpos_attention_kernel(const AttnArgs p) {
   using S = AttnShape<D>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[S::LDS_BYTES / 2];
   uint16_t* sK = lds;                      // [32 keys][DP]
