@@ -41,7 +41,56 @@ DEVI float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)
 DEVI int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 DEVI int lane_id() { return threadIdx.x & 63; }
 
+// ---- cross-lane reductions on DPP lane moves (within rows of 16 lanes) and v_readlane, without the LDS round trip
+// of a bpermute shuffle. Each gives the xor-butterfly reduction's result (v op= shfl_xor(v, 1), 2, 4, ...) bit for
+// bit: every level combines the same two partial results, at most in commuted order.
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm(1, 0, 3, 2): lane ^ 1
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm(2, 3, 0, 1): lane ^ 2
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i of each 8 <- lane 7 - i (lane ^ 4 once quads are uniform)
+constexpr int DPP_ROR4 = 0x124;        // row_ror:4, lane i of each 16 <- lane i - 4
+constexpr int DPP_ROR8 = 0x128;        // row_ror:8
+template <int CTRL>
+DEVI float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+DEVI float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
+
+// over each aligned group of 8 lanes, in every lane of the group
+DEVI float group8_sum(float v) {
+  v += dpp_mov<DPP_XOR1>(v);
+  v += dpp_mov<DPP_XOR2>(v);
+  return v + dpp_mov<DPP_HALF_MIRROR>(v);
+}
+DEVI float group8_max(float v) {
+  v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_mov<DPP_XOR2>(v));
+  return fmaxf(v, dpp_mov<DPP_HALF_MIRROR>(v));
+}
+// over each row of 16 lanes, in every lane of the row (the row's total in lane 15 is the butterfly's order)
+DEVI float row16_sum(float v) {
+  v += dpp_mov<DPP_XOR1>(v);
+  v += dpp_mov<DPP_XOR2>(v);
+  v += dpp_mov<DPP_ROR4>(v);
+  return v + dpp_mov<DPP_ROR8>(v);
+}
+DEVI float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
+  v = fmaxf(v, dpp_mov<DPP_XOR2>(v));
+  v = fmaxf(v, dpp_mov<DPP_ROR4>(v));
+  return fmaxf(v, dpp_mov<DPP_ROR8>(v));
+}
+// over the 64 lanes (all active), the same value in every lane
+DEVI float wave_sum64(float v) {
+  v = row16_sum(v);
+  return (lane_value(v, 15) + lane_value(v, 31)) + (lane_value(v, 47) + lane_value(v, 63));
+}
+DEVI float wave_max64(float v) {
+  v = row16_max(v);
+  return fmaxf(fmaxf(lane_value(v, 15), lane_value(v, 31)), fmaxf(lane_value(v, 47), lane_value(v, 63)));
+}
+
 DEVI float wave_max_xor(float v, int width) {
+  if (width == 64) return wave_max64(v);
   for (int o = 1; o < width; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }

@@ -134,18 +134,8 @@ DEVI void unpack_bf(const uint4& a, const uint4& b, float (&f)[16]) {
 }
 
 // group-of-8 reductions (lanes 8g .. 8g+7 of a wave)
-DEVI float group_sum(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  return v;
-}
-DEVI float group_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 1, 64));
-  v = fmaxf(v, __shfl_xor(v, 2, 64));
-  v = fmaxf(v, __shfl_xor(v, 4, 64));
-  return v;
-}
+DEVI float group_sum(float v) { return group8_sum(v); }
+DEVI float group_max(float v) { return group8_max(v); }
 
 // the 16 values a lane holds of a 128-vector as int8 with the vector's scale (absmax / 127 over the 8 lanes)
 DEVI void store16_q8(const float (&f)[16], int8_t* dst, float* scale, int gl) {
@@ -288,12 +278,10 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
   if (tid < 64) {
     const float mg = sm[tid];
     float M = mg;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+    M = wave_max64(M);
     const float w = M == -INFINITY ? 0.f : __expf(mg - M);
     float L = w * sl[tid];
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) L += __shfl_xor(L, o, 64);
+    L = wave_sum64(L);
     sw[tid] = w;
     if (tid == 0) {
       sML[0] = M;
@@ -434,8 +422,7 @@ __global__ void __launch_bounds__(256) dec_scatter_kv_kernel(const uint16_t* __r
       f[k] = __uint_as_float(k & 1 ? w[k >> 1] & 0xffff0000u : w[k >> 1] << 16);
       mx = fmaxf(mx, fabsf(f[k]));
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    mx = row16_max(mx);
     if (!live) return;
     const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
     uint32_t q[2] = {0, 0};

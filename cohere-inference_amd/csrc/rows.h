@@ -51,10 +51,7 @@ DEVI void store_q8(const Row<VEC>& r, int cols, int lane, int8_t* q, float* scal
   if (lane == 0) *scale = s;
 }
 
-DEVI float wave_sum(float v) {
-  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+DEVI float wave_sum(float v) { return wave_sum64(v); }
 
 // a LayerNorm's weight and bias as this lane's 16-byte chunks (bf16), loaded before the row's statistics so that no
 // load waits behind them
