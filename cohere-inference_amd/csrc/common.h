@@ -89,6 +89,25 @@ DEVI float wave_max64(float v) {
   return fmaxf(fmaxf(lane_value(v, 15), lane_value(v, 31)), fmaxf(lane_value(v, 47), lane_value(v, 63)));
 }
 
+// v combined with lane ^ 16's / lane ^ 32's value (gfx950 v_permlane16_swap / v_permlane32_swap: with both operands
+// v, the two results hold, in every lane, its own and its partner's value), as v op shfl_xor(v, 16 / 32)
+DEVI float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+DEVI float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+DEVI float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+DEVI float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 DEVI float wave_max_xor(float v, int width) {
   if (width == 64) return wave_max64(v);
   for (int o = 1; o < width; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

@@ -17,6 +17,7 @@
 #include "rows.h"
 
 #include <string>
+#include <type_traits>
 
 namespace {
 
@@ -365,13 +366,33 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
       }
     }
   }
-  for (int o = 1; o < 64; o <<= 1) {
-    const float ob = __shfl_xor(best, o, 64);
-    const int oa = __shfl_xor(arg, o, 64);
+  // the wave's (maximum, first index): pairs combined across lane ^ 1, 2, 4, 8 (DPP lane moves; the combination is
+  // symmetric, so each lane group holds one pair before the next level) and ^ 16, 32 (permlane swaps: both results
+  // are the group's and its partner's pair, in some order)
+  auto take = [&](float ob, int oa) {
     if (ob > best || (ob == best && oa < arg)) {
       best = ob;
       arg = oa;
     }
+  };
+  auto dpp_i = [](auto ctrl, int v) { return __builtin_amdgcn_update_dpp(0, v, decltype(ctrl)::value, 0xF, 0xF, false); };
+  take(dpp_mov<DPP_XOR1>(best), dpp_i(std::integral_constant<int, DPP_XOR1>{}, arg));
+  take(dpp_mov<DPP_XOR2>(best), dpp_i(std::integral_constant<int, DPP_XOR2>{}, arg));
+  take(dpp_mov<DPP_HALF_MIRROR>(best), dpp_i(std::integral_constant<int, DPP_HALF_MIRROR>{}, arg));
+  take(dpp_mov<DPP_ROR8>(best), dpp_i(std::integral_constant<int, DPP_ROR8>{}, arg));
+  {
+    const auto b2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(best), __float_as_uint(best), false, false);
+    const auto a2 = __builtin_amdgcn_permlane16_swap((unsigned)arg, (unsigned)arg, false, false);
+    best = __uint_as_float(b2[0]);
+    arg = (int)a2[0];
+    take(__uint_as_float(b2[1]), (int)a2[1]);
+  }
+  {
+    const auto b2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(best), __float_as_uint(best), false, false);
+    const auto a2 = __builtin_amdgcn_permlane32_swap((unsigned)arg, (unsigned)arg, false, false);
+    best = __uint_as_float(b2[0]);
+    arg = (int)a2[0];
+    take(__uint_as_float(b2[1]), (int)a2[1]);
   }
   if ((tid & 63) == 0) {
     sb[tid >> 6] = best;

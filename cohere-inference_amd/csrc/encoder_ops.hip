@@ -315,8 +315,7 @@ relpos_attention_kernel(const AttnArgs p) {
         sv[kb * 4 + e] = v;
         mx = fmaxf(mx, v);
       }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx = xor32_max(xor16_max(mx));
     const float alpha = __expf(m - mx);
     m = mx;
     float rs = 0.f;
@@ -327,8 +326,7 @@ relpos_attention_kernel(const AttnArgs p) {
       rs += e;
       pb[k] = (__bf16)e;
     }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
+    rs = xor32_sum(xor16_sum(rs));
     l = l * alpha + rs;
 #pragma unroll
     for (int ob = 0; ob < S::OB; ++ob) {

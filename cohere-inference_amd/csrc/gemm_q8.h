@@ -609,12 +609,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
               acc[j][i][4 * q + r] = __float_as_int(u);
             }
           }
-          if constexpr (MS == 16) {
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          } else {
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          }
+          if constexpr (MS == 16) mx = xor32_max(xor16_max(mx));
+          else mx = xor32_max(mx);
           if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
         }
       __syncthreads();
