@@ -696,8 +696,8 @@ void launch_tile(const GemmArgs& p, hipStream_t s) {
 //   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
 //   5 32x128 (1x4, 4)    6 256x256 (2x4, 2 dense / 3 sparse)        7 64x64 (2x2, 4)    8 256x128 (4x2, 3)
 //   9 128x256 (2x4, 3)   10 256x256 (4x2, 2 dense / 3 sparse)   11 256x128 (2x2, 3)   12 128x128 (2x2, 4)
-//   13 128x256 (2x2, 3)   14 256x256 (2x2, 2 dense / 3 sparse); tiles 11-13 use the 32x32 matrix instructions,
-//   the others 16x16
+//   13 128x256 (2x2, 3)   14 256x256 (2x2, 2 dense / 3 sparse)   15 256x256 (4x4: 16 waves, 2 dense / 3 sparse);
+//   tiles 11-13 use the 32x32 matrix instructions, the others 16x16
 struct TileInfo {
   int bm, bn;
   bool grouped_ok;
@@ -705,7 +705,7 @@ struct TileInfo {
 constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
                               {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
                               {256, 128, true}, {128, 256, true},  {256, 256, false}, {256, 128, false},
-                              {128, 128, true}, {128, 256, false}, {256, 256, false}};
+                              {128, 128, true}, {128, 256, false}, {256, 256, false}, {256, 256, false}};
 constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
 
 // launches tile `tile` for one (SPARSE, EPI, GROUPED); false when the tile has no such instantiation
@@ -731,6 +731,7 @@ bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
       case 11: launch_tile<256, 128, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
       case 13: launch_tile<128, 256, 2, 2, 3, 32, EPI, false, SPARSE>(p, s); return true;
       case 14: launch_tile<256, 256, 2, 2, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
+      case 15: launch_tile<256, 256, 4, 4, SPARSE ? 3 : 2, 16, EPI, false, SPARSE>(p, s); return true;
       default: break;
     }
   }
