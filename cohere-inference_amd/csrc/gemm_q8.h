@@ -280,13 +280,17 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   // with the next group's instructions, the fold reads results finished long before, so the matrix cores keep going.
   auto group_scale = [&](int g, int i) {
     const int r = tok(i);
-    return scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
+    // GS > 0 is launched only when every group's scales are in LDS: a plain LDS read (a select between the two
+    // pointers makes the compiler read through a flat pointer)
+    if constexpr (GS > 0) return sS[g * BM + r];
+    else return scales_in_lds ? sS[g * BM + r] : p.sx[(int64_t)min(m0 + r, M - 1) * p.ldsx + g];
   };
+  // the finished group of block (j, i) into fp32; the next group's first matrix instruction then takes a zero
+  // accumulator (mma_block's `fresh`), so the int32 accumulators are not cleared with register moves
   auto fold_block = [&](int j, int i, float sc) {
     if constexpr (GROUPED) {
 #pragma unroll
       for (int q = 0; q < RPL; ++q) accf[j][i][q] = __builtin_fmaf((float)acc[j][i][q], sc, accf[j][i][q]);
-      acc[j][i] = Acc{};
     }
   };
 
@@ -329,21 +333,22 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     }
   };
   int kstep = 0;
-  auto mma_block = [&](const Frags& F, int j, int i) {
+  auto mma_block = [&](const Frags& F, int j, int i, bool fresh = false) {
+    const Acc c = fresh ? Acc{} : acc[j][i];
     if constexpr (BF && MS == 16)
       acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, F.aw[j]),
-                                                         __builtin_bit_cast(v8bf, F.bx[i]), acc[j][i], 0, 0, 0);
+                                                         __builtin_bit_cast(v8bf, F.bx[i]), c, 0, 0, 0);
     else if constexpr (BF)
       acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, F.aw[j]),
-                                                         __builtin_bit_cast(v8bf, F.bx[i]), acc[j][i], 0, 0, 0);
+                                                         __builtin_bit_cast(v8bf, F.bx[i]), c, 0, 0, 0);
     else if constexpr (SPARSE && MS == 16)
-      acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+      acc[j][i] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(F.aw[j], F.bx[i], c, F.ix[j], 0, 0);
     else if constexpr (SPARSE)
-      acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], acc[j][i], F.ix[j], 0, 0);
+      acc[j][i] = __builtin_amdgcn_smfmac_i32_32x32x64_i8(F.aw[j], F.bx[i], c, F.ix[j], 0, 0);
     else if constexpr (MS == 16)
-      acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
+      acc[j][i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(F.aw[j], F.bx[i], c, 0, 0, 0);
     else
-      acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.aw[j], F.bx[i], acc[j][i], 0, 0, 0);
+      acc[j][i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(F.aw[j], F.bx[i], c, 0, 0, 0);
   };
   // one K step; with fold, the finished group gprev is folded block by block just before the block's instruction
   auto mma_step = [&](const Frags& F, bool fold, int gprev) {
@@ -356,7 +361,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
           fold_block(j, i, gsc[i]);
-          mma_block(F, j, i);
+          mma_block(F, j, i, true);
         }
       return;
     }
@@ -684,7 +689,7 @@ void launch_tile(const GemmArgs& p, hipStream_t s) {
   // two, its unrolled groups do not fit the registers)
   constexpr int GS = 256 / Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::KSTEP;
   if constexpr (GROUPED && EPI == EPI_RESID && WM * WN <= 4) {
-    if (p.group == 256) {
+    if (p.group == 256 && p.K / 256 <= Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::GMAX) {  // scales all in LDS
       gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE, GS><<<grid, WM * WN * 64, 0, s>>>(p);
       return;
     }
