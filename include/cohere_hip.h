@@ -42,8 +42,10 @@ enum {
  *   SILU_Q8  out int8 [M, N] and qs fp32 [M, N / G] (ldqs), G = the column tile of the reference config cfg
  *            (64 for cfg 5 and 9, 256 for 4, 6 and 8, else 128; 256 when cfg < 0)
  *   I32      out int32 [M, N] raw accumulators (group == K only)
- * Requirements: K % 64 == 0, group % 64 == 0, K % group == 0, N % 64 == 0. cfg is the reference's tile-config id
- * (0, 1, 3-10; unknown ids are rejected) or -1; it never changes the result (tiles are chosen for gfx950 here). */
+ * Requirements: K % 64 == 0, group % 64 == 0, K % group == 0, N % 64 == 0; a, w, sw 16-byte aligned with lda % 16 ==
+ * 0; out rows 16-byte aligned (out and ldc x element size); bias 8-byte aligned; resid 16-byte aligned, ldr % 8 == 0.
+ * cfg is the reference's tile-config id (0, 1, 3-10; unknown ids are rejected) or -1; it never changes the result
+ * (tiles are chosen for gfx950 here). */
 int cohere_gemm_i8(const int8_t* a, int64_t lda, const float* sa, int64_t ldsa, int64_t group, const int8_t* w,
                    const float* sw, const uint16_t* bias, void* out, int64_t ldc, int32_t epi, const uint16_t* resid,
                    int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N, int64_t K, int32_t cfg,
@@ -53,8 +55,9 @@ int cohere_gemm_i8(const int8_t* a, int64_t lda, const float* sa, int64_t ldsa, 
  * widens it to gemm_i8's epilogues. x int8 [M, K] (ldx) with sx fp32 [M, K / group] (ldsx); the 2:4 weights as
  * kernels/sparse.py compress_24 stores them: wc int8 [N, K / 2] kept values, e int32 [N, K / 32] selectors (a nibble
  * i0 | i1 << 2 per group of four, lowest K in the lowest nibble) -- exactly the CDNA4 SMFMAC A operand and index
- * format, used as is. Epilogues and outputs as cohere_gemm_i8. Requirements: K % 128 == 0, group % 128 == 0,
- * K % group == 0, N % 64 == 0. The result equals cohere_gemm_i8 on the decompressed weights, bit for bit.
+ * format, used as is. Epilogues, outputs and alignment as cohere_gemm_i8 (e 16-byte aligned too). Requirements:
+ * K % 128 == 0, group % 128 == 0, K % group == 0, N % 64 == 0. The result equals cohere_gemm_i8 on the decompressed
+ * weights, bit for bit.
  * cfg: the reference's sparse config id (0-4) or -1. */
 int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, int64_t group, const int8_t* wc,
                    const int32_t* e, const float* sw, const uint16_t* bias, void* out, int64_t ldc, int32_t epi,
