@@ -159,6 +159,26 @@ def cpu_baseline(target_s=10.0):
         torch._int_mm(a1, b1)
         torch._int_mm(a2, b2)
         best = min(best, time.perf_counter() - t)
+    torch.set_num_threads(1)
+    t = time.perf_counter()
+    torch._int_mm(a1, b1)
+    torch._int_mm(a2, b2)
+    one = time.perf_counter() - t
+    torch.set_num_threads(threads)
+    # config 3's decoder projections (M=64, int8 weights as int32-accumulating matmuls): one step's 49 calls
+    g = torch.Generator().manual_seed(3)
+    dec = [(3072, 1024)] + [(1024, 1024)] * 3 + [(4096, 1024), (1024, 4096)]
+    xs64 = {k: torch.randint(-127, 128, (64, k), generator=g, dtype=torch.int8) for k in (1024, 4096)}
+    ws64 = [torch.randint(-127, 128, (k, n), generator=g, dtype=torch.int8) for n, k in dec]
+    head = torch.randint(-127, 128, (1024, 16384), generator=g, dtype=torch.int8)
+    dec_best, dec_bytes = 1e9, 8 * sum(n * k for n, k in dec) + 16384 * 1024
+    for _ in range(3):
+        t = time.perf_counter()
+        for _layer in range(8):
+            for (n, k), w in zip(dec, ws64):
+                torch._int_mm(xs64[k], w)
+        torch._int_mm(xs64[1024], head)
+        dec_best = min(dec_best, time.perf_counter() - t)
     model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -172,7 +192,12 @@ def cpu_baseline(target_s=10.0):
                       f"weights, bias epilogue) in {dt * steps:.1f} s, oracle/cohere_oracle.c",
             "cpu_model": model,
             "reference_cpu_path_int_mm": {"value": round(ops / best / 1e12, 4), "unit": "TOPS", "threads": threads,
-                                          "what": "torch._int_mm on the same step, int32 result only, best of 3"}}
+                                          "what": "torch._int_mm on the same step, int32 result only, best of 3",
+                                          "value_1_thread": round(ops / one / 1e12, 4)},
+            "reference_cpu_path_decoder_gemms": {"ms_per_step": round(dec_best * 1e3, 2),
+                                                 "GBps": round(dec_bytes / dec_best / 1e9, 1), "threads": threads,
+                                                 "what": "torch._int_mm on config 3's 49 step projections at M=64 "
+                                                         "(int8 weights, int32 result), best of 3"}}
 
 
 def decoder_extra(dev, reps_sets=4):
