@@ -97,7 +97,8 @@ def test_gemm_every_tile_same_bits(ext):
 
 # ---- a3 / a4: epilogues ---------------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("M,N,K", [(3000, 5120, 1280), (3000, 1280, 5120), (45, 3840, 1280)])
+# 12032 rows: config 4's encoder call (32 clips of 376 frames in one call), the largest M the pipeline runs
+@pytest.mark.parametrize("M,N,K", [(3000, 5120, 1280), (3000, 1280, 5120), (45, 3840, 1280), (12032, 5120, 1280)])
 def test_gemm_bias_bit_exact(ext, M, N, K):
     from kernels.cuda_ext import EPI_BIAS
 
@@ -191,7 +192,7 @@ def _sparse_weights(N, K, seed):
 
 
 @pytest.mark.parametrize("M,N,K,group", [(3000, 5120, 1280, 1280), (3000, 1280, 5120, 5120), (3000, 1280, 5120, 256),
-                                         (5, 256, 128, 128), (130, 640, 1024, 512)])
+                                         (5, 256, 128, 128), (130, 640, 1024, 512), (12032, 1280, 5120, 256)])
 def test_sparse_equals_dense_on_pruned(ext, M, N, K, group):
     from kernels.cuda_ext import EPI_BIAS, EPI_I32, EPI_RESID
 
