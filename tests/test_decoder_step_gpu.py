@@ -110,6 +110,38 @@ def test_dec_attention_bf16(gpu):
     assert np.array_equal(bf16_bits(gk), ck) and np.array_equal(bf16_bits(gv), cv)
 
 
+@pytest.mark.parametrize("q8", [True, False])
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_dec_attention_long_caches(gpu, q8, self_attn):
+    """Caches longer than one pass of the kernel (512 int8 / 256 bf16 keys per pass): the online softmax's rescale
+    across passes, with lengths on and around the pass boundaries."""
+    g = torch.Generator().manual_seed(11 + 2 * q8 + self_attn)
+    slots, H, T = 7, 8, 1300
+    n_self = [1299, 512, 513, 1024, 256, 257, 700]
+    n_cross = [1300, 512, 513, 1025, 256, 257, 1]
+    n = torch.tensor(n_self if self_attn else n_cross, dtype=torch.int32)
+    active = torch.tensor([0, 1, 2, 3, 4, 5, 6], dtype=torch.int32)
+    rows = active.numel()
+    q = torch.randn(rows, (3 if self_attn else 1) * H * 128, generator=g).to(torch.bfloat16)
+    out = torch.empty(rows, H * 128, dtype=torch.bfloat16, device=gpu)
+    if q8:
+        k8, v8, ks, vs = _caches(g, slots, H, T)
+        gk, gv, gks, gvs = (t.to(gpu) for t in (k8, v8, ks, vs))
+        _ext().dec_attention_q8(self_attn, active.to(gpu), q.to(gpu), gk, gv, gks, gvs, n.to(gpu), 128 ** -0.5, 1,
+                                None, out)
+        ck, cv, cks, cvs = (t.numpy().copy() for t in (k8, v8, ks, vs))
+        want = oracle.dec_attention(self_attn, active.numpy(), _bf(q), n.numpy(), 128 ** -0.5, k8=ck, v8=cv,
+                                    ks=cks, vs=cvs)
+    else:
+        k = torch.randn(slots, H, T, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(slots, H, T, 128, generator=g).to(torch.bfloat16)
+        gk, gv = k.to(gpu), v.to(gpu)
+        _ext().dec_attention(self_attn, active.to(gpu), q.to(gpu), gk, gv, n.to(gpu), 0.05, 1, None, out)
+        ck, cv = bf16_bits(k).copy(), bf16_bits(v).copy()
+        want = oracle.dec_attention(self_attn, active.numpy(), _bf(q), n.numpy(), 0.05, k=ck, v=cv)
+    _close(bf16_bits(out), want)
+
+
 def test_dec_pick_exact(gpu):
     g = torch.Generator().manual_seed(8)
     rows, V, S = 7, 16384, 10
