@@ -61,9 +61,12 @@ struct GemmArgs {
   int qgroup;            // SILU_Q8 columns per scale
   int epi;               // host-side dispatch only: the kernels take the epilogue as a template parameter
   float alpha;
+  int xcd_rows;          // > 0: the token tiles split into xcd_rows parts and the channel tiles into 8 / xcd_rows,
+                         // one part each per XCD (set by launch_tile); 0: contiguous tile ranges per XCD
 };
 
 constexpr int LDS_BYTES = 160 * 1024;
+inline bool g_xcd_split = true;  // tuning hook (cohere_set_gemm_tile with tile -2 / -3 switches it)
 
 template <int BM, int BN, int WM, int WN, int ST, int MS, bool GROUPED, bool SPARSE>
 struct Tile {
@@ -157,14 +160,25 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 
   const int M = p.M, N = p.N, K = p.K;
   const int ntm = (M + BM - 1) / BM, ntn = N / BN, ntiles = ntm * ntn;
-  int t;
-  {  // XCD-aware remap: workgroup b runs on XCD b % 8; give each XCD a contiguous range of logical tiles
-    const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, per = ntiles >> 3, rem = ntiles & 7;
-    t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+  int m0, n0;
+  if (p.xcd_rows > 0) {
+    // workgroup b runs on XCD b % 8: XCD x takes token part x / (8 / xcd_rows) and channel part x % (8 / xcd_rows)
+    // of the tile grid, so each XCD's L2 fetches only its part's tokens and weights (the grid divides evenly)
+    const int parts_n = 8 / p.xcd_rows, rm = ntm / p.xcd_rows, rn = ntn / parts_n;
+    const int xcd = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    m0 = ((xcd / parts_n) * rm + idx % rm) * BM;
+    n0 = ((xcd % parts_n) * rn + idx / rm) * BN;
+  } else {
+    int t;
+    {  // XCD-aware remap: workgroup b runs on XCD b % 8; give each XCD a contiguous range of logical tiles
+      const int b = blockIdx.x, xcd = b & 7, idx = b >> 3, per = ntiles >> 3, rem = ntiles & 7;
+      t = xcd < rem ? xcd * (per + 1) + idx : rem * (per + 1) + (xcd - rem) * per + idx;
+    }
+    constexpr int GM = 8;
+    const int gw = GM * ntn, first = (t / gw) * GM, gs = min(ntm - first, GM);
+    m0 = (first + (t % gw) % gs) * BM;
+    n0 = ((t % gw) / gs) * BN;
   }
-  constexpr int GM = 8;
-  const int gw = GM * ntn, first = (t / gw) * GM, gs = min(ntm - first, GM);
-  const int m0 = (first + (t % gw) % gs) * BM, n0 = ((t % gw) / gs) * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int wm = wave / WN, wn = wave % WN;
@@ -682,9 +696,26 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   }
 }
 
+// the XCD split of launch_tile: among the splits of the tile grid into xcd_rows x (8 / xcd_rows) equal parts, the one
+// whose L2 fetches are fewest (tokens fetched once per channel part, weights once per token part); 0 when the grid
+// does not split evenly
+inline int xcd_split(int ntm, int ntn, double x_bytes, double w_bytes) {
+  int best = 0;
+  double cost = 0.0;
+  for (int a = 1; a <= 8; a *= 2) {
+    if (ntm % a != 0 || ntn % (8 / a) != 0) continue;
+    const double c = (8 / a) * x_bytes + a * w_bytes;
+    if (best == 0 || c < cost) best = a, cost = c;
+  }
+  return best;
+}
+
 template <int BM, int BN, int WM, int WN, int ST, int MS, int EPI, bool GROUPED, bool SPARSE, bool BF = false>
-void launch_tile(const GemmArgs& p, hipStream_t s) {
-  const int grid = ((p.M + BM - 1) / BM) * (p.N / BN);
+void launch_tile(const GemmArgs& args, hipStream_t s) {
+  const int ntm = (args.M + BM - 1) / BM, ntn = args.N / BN, grid = ntm * ntn;
+  GemmArgs p = args;
+  p.xcd_rows = g_xcd_split ? xcd_split(ntm, ntn, (double)p.M * p.K,
+                                       SPARSE ? (double)p.N * p.K * 0.625 : (double)p.N * p.K) : 0;
   // the feed-forward W2's grouping (256 K per scale) runs the static-group loop (tiles of one wave per SIMD: with
   // two, its unrolled groups do not fit the registers)
   constexpr int GS = 256 / Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::KSTEP;

@@ -258,7 +258,8 @@ const char* cohere_last_error(void);
 const char* cohere_version(void);
 
 /* Tuning hook (no counterpart in the reference): force the gfx950 tile of the int8 GEMMs (-1 = automatic choice by
- * shape). Used by bench.py's sweeps; results never depend on it. Returns the number of tiles available. */
+ * shape; -2 / -3 switch off / on the split of evenly divisible tile grids into one part per XCD, on by default).
+ * Used by bench.py's sweeps; results never depend on it. Returns the number of tiles available. */
 int cohere_set_gemm_tile(int32_t tile);
 
 /* Tuning hook (no counterpart in the reference): force the skinny projections' workgroup shape -- strips of 16
