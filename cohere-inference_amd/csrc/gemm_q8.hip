@@ -40,13 +40,14 @@ int choose_tile(const GemmArgs& p, bool grouped, bool bf = false) {
   // tile on 32x32 instructions (12) precedes its 16x16 twin (0). Grouped scales skip 12 and the 8-wave tiles (8, 9,
   // whose fold accumulators spill): 0 is the fastest grouped tile from 3000 to 12032 rows (12032: 154 us against
   // 206-224 us for 8 and 9).
-  // SILU_Q8's epilogue is VALU-heavy: its 256x256 tile runs 16 waves (15) in place of 8 (6), four per SIMD hiding more
-  // of its latency (config 1: 31.7 -> 30.3 us; the bias epilogues are faster with 8)
+  // The int8 256x256 tile runs 16 waves (15) in place of 8 (6), four per SIMD hiding more latency: SILU_Q8's
+  // VALU-heavy epilogue 31.7 -> 30.3 us at config 1; with the grid split into one part per XCD, the bias epilogue too
+  // (config 1 up 22.8 -> 21.9 us, config 0 dense 24.5 -> 24.1 us)
   static const int order[] = {6, 9, 1, 8, 2, 12, 0, 4, 3, 5, 7};
   const int64_t want = (int64_t)num_cus() * 64 / 100;
   int best = -1;
   for (int id0 : order) {
-    const int id = id0 == 6 && p.epi == EPI_SILU_Q8 && !bf ? 15 : id0;
+    const int id = id0 == 6 && !bf ? 15 : id0;
     if (!fits(id) || (grouped && (id == 12 || id == 8 || id == 9))) continue;
     if (tiles_of(id) >= want) return id;
     if (best < 0 || tiles_of(id) > tiles_of(best)) best = id;
