@@ -376,9 +376,7 @@ def decoder_step_extra(dev, steps=448):
         e1.record()
     dec.stream.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    weights = sum(t.numel() * t.element_size() for ly in dec.layers
-                  for t in (ly.qkv_w8[0], ly.fc1_w8[0], ly.fc2_w8[0], ly.o[0], ly.cq[0], ly.co[0]))
-    weights += dec.head_w8[0].numel()
+    weights = dec.weight_bytes()
     mean_len = (len0 + float(dec.pos[:B].float().mean())) / 2  # over the timed steps
     kv = 8 * B * 2 * 1024 * (mean_len + F_)  # int8 keys + values read per step (8 layers), scales aside
     return {"what": "config 3: one captured decoder step, 64 active slots, self-KV lengths U(1..448), cross-attention "

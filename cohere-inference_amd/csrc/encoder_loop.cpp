@@ -4,7 +4,8 @@
 // interpreter and argument parsing; here the loop is native.
 //
 // Per layer (x (rows, 1280) bf16 in place; hq/hs the int8 rows and scales feeding the next GEMM):
-//   FF1:  tq, ts = SILU_Q8(hq W1);  x = x + 0.5 (tq W2)          (W2 2:4 sparse when its compressed weights are given)
+//   FF1:  tq, ts = SILU_Q8(hq W1);  x = x + 0.5 (tq W2)          (W1 / W2 2:4 sparse when their compressed weights
+//                                                                  are given)
 //   ATT:  hq = LN_att(x);  qkv = hq Wqkv + b;  a = relpos_attention(qkv);  hq = q8(a);  x = x + (hq Wo + bo)
 //   CONV: hq = LN_conv(x); a = GLU(hq Wpw1 + b);  hq = q8(silu(bn(dwconv(a))));  x = x + (hq Wpw2 + b)
 //   FF2:  hq = LN_ff2(x);  as FF1
@@ -12,6 +13,7 @@
 #include "cohere_hip.h"
 #include "common.h"
 
+#include <algorithm>
 #include <string>
 
 namespace {
@@ -24,6 +26,8 @@ enum F {
   Q_FF1_W1, Q_FF1_S1, Q_FF1_W2, Q_FF1_S2, Q_FF2_W1, Q_FF2_S1, Q_FF2_W2, Q_FF2_S2, Q_QKV_W, Q_QKV_S, Q_PW1_W, Q_PW1_S,
   Q_O_W, Q_O_S, Q_PW2_W, Q_PW2_S,
   SP_FF1_W, SP_FF1_E, SP_FF2_W, SP_FF2_E,
+  // this library's own: the first feed-forward linears in 2:4 form (the reference keeps them dense)
+  SP_FF1_W1, SP_FF1_E1, SP_FF2_W1, SP_FF2_E1,
   N_FIELDS
 };
 static_assert(N_FIELDS == COHERE_ENC_N_FIELDS, "field count");
@@ -42,6 +46,30 @@ struct Workspace {
   float* ts;      // (rows, 5120 / group)
   int64_t bytes;
 };
+
+// the bf16 branch's buffers: LayerNorm output, feed-forward hidden, QKV, attention / GLU output, depthwise output
+struct WorkspaceBf16 {
+  uint16_t *h, *t, *qkv, *a, *z;
+  int64_t bytes;
+};
+
+WorkspaceBf16 carve_bf16(void* base, int64_t rows) {
+  WorkspaceBf16 w{};
+  char* p = static_cast<char*>(base);
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    char* r = p ? p + off : nullptr;
+    off += align256(bytes);
+    return reinterpret_cast<uint16_t*>(r);
+  };
+  w.h = take(rows * DM * 2);
+  w.t = take(rows * DFF * 2);
+  w.qkv = take(rows * DQKV * 2);
+  w.a = take(rows * DM * 2);
+  w.z = take(rows * DM * 2);
+  w.bytes = off;
+  return w;
+}
 
 Workspace carve(void* base, int64_t rows, int64_t group) {
   Workspace w{};
@@ -71,8 +99,83 @@ const T* fld(const void* const* ly, int f) {
 
 extern "C" int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group) {
   if (rows < 0 || group <= 0 || DFF % group) return -1;
-  return carve(nullptr, rows, group).bytes;
+  return std::max(carve(nullptr, rows, group).bytes, carve_bf16(nullptr, rows).bytes);
 }
+
+namespace {
+
+// The bf16 branch (reference kernels/csrc/encoder_loop.cpp:101-124): every linear a bf16 GEMM with its epilogue
+// fused (SiLU, residual, GLU), the LayerNorms, the attention and the depthwise convolution in bf16.
+int encoder_layers_bf16(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers, const double* eps,
+                        const int32_t* tiles, int64_t n_tiles, const int32_t* lo, const int32_t* hi, int64_t rel_off,
+                        int64_t max_len, int64_t rel_rows, double scale, int32_t heads, int32_t head_dim,
+                        int64_t c_bf, const WorkspaceBf16& ws, void* stream) {
+  static const int required[] = {LN_FF1_W, LN_FF1_B, LN_ATT_W, LN_ATT_B, LN_CONV_W, LN_CONV_B, LN_FF2_W, LN_FF2_B,
+                                 LN_OUT_W, LN_OUT_B, FF1_W1, FF1_W2, FF2_W1, FF2_W2, WQKV, WO, BU, BV, RK, WPW1,
+                                 WDW, BDW, BN_SCALE, BN_SHIFT, WPW2};
+  for (int64_t l = 0; l < n_layers; ++l)
+    for (int f : required)
+      COHERE_REQUIRE(fields[l * N_FIELDS + f],
+                     "encoder_layers (bf16): layer " + std::to_string(l) + " misses field " + std::to_string(f));
+  auto ep = [&](int64_t i, int e) { return (float)eps[i * N_EPS + e]; };
+  int64_t i = 0;
+  auto fail = [&](const char* what) {
+    cohere::set_error("encoder_layers (bf16): layer " + std::to_string(i) + ", " + what + ": " + cohere_last_error());
+    return 1;
+  };
+#define RUN(call, what) \
+  if ((call) != 0) return fail(what)
+  auto gemm = [&](const uint16_t* a, int64_t k, const void* const* ly, int w, int b, uint16_t* out, int64_t ldc,
+                  int epi, int64_t n, float alpha) {
+    return cohere_gemm_bf16(a, k, fld<uint16_t>(ly, w), fld<uint16_t>(ly, b), out, ldc, epi,
+                            epi == COHERE_EPI_RESID ? out : nullptr, ldc, alpha, rows, n, k, (int32_t)c_bf, stream);
+  };
+  RUN(cohere_layernorm(x, DM, fld<uint16_t>(fields, LN_FF1_W), fld<uint16_t>(fields, LN_FF1_B), ep(0, EPS_FF1),
+                       nullptr, nullptr, 0.f, ws.h, DM, rows, DM, stream),
+      "first LayerNorm");
+  for (i = 0; i < n_layers; ++i) {
+    const void* const* ly = fields + i * N_FIELDS;
+    RUN(gemm(ws.h, DM, ly, FF1_W1, FF1_B1, ws.t, DFF, COHERE_EPI_SILU, DFF, 1.f), "feed-forward 1 W1");
+    RUN(gemm(ws.t, DFF, ly, FF1_W2, FF1_B2, x, DM, COHERE_EPI_RESID, DM, 0.5f), "feed-forward 1 W2");
+    RUN(cohere_layernorm(x, DM, fld<uint16_t>(ly, LN_ATT_W), fld<uint16_t>(ly, LN_ATT_B), ep(i, EPS_ATT), nullptr,
+                         nullptr, 0.f, ws.h, DM, rows, DM, stream),
+        "attention LayerNorm");
+    RUN(gemm(ws.h, DM, ly, WQKV, BQKV, ws.qkv, DQKV, COHERE_EPI_BIAS, DQKV, 1.f), "QKV");
+    RUN(cohere_relpos_attention(ws.qkv, fld<uint16_t>(ly, RK), rel_rows, fld<uint16_t>(ly, BU),
+                                fld<uint16_t>(ly, BV), tiles, n_tiles, heads, head_dim, rel_off, max_len,
+                                (float)scale, ws.a, stream),
+        "attention");
+    RUN(gemm(ws.a, DM, ly, WO, BO, x, DM, COHERE_EPI_RESID, DM, 1.f), "attention output projection");
+    RUN(cohere_layernorm(x, DM, fld<uint16_t>(ly, LN_CONV_W), fld<uint16_t>(ly, LN_CONV_B), ep(i, EPS_CONV),
+                         nullptr, nullptr, 0.f, ws.h, DM, rows, DM, stream),
+        "convolution LayerNorm");
+    RUN(gemm(ws.h, DM, ly, WPW1, BPW1, ws.a, DM, COHERE_EPI_GLU, 2 * DM, 1.f), "pointwise conv 1 (GLU)");
+    RUN(cohere_dwconv_bn_silu(ws.a, fld<float>(ly, WDW), fld<float>(ly, BDW), fld<float>(ly, BN_SCALE),
+                              fld<float>(ly, BN_SHIFT), lo, hi, ws.z, rows, DM, 9, stream),
+        "depthwise conv");
+    RUN(gemm(ws.z, DM, ly, WPW2, BPW2, x, DM, COHERE_EPI_RESID, DM, 1.f), "pointwise conv 2");
+    RUN(cohere_layernorm(x, DM, fld<uint16_t>(ly, LN_FF2_W), fld<uint16_t>(ly, LN_FF2_B), ep(i, EPS_FF2), nullptr,
+                         nullptr, 0.f, ws.h, DM, rows, DM, stream),
+        "feed-forward 2 LayerNorm");
+    RUN(gemm(ws.h, DM, ly, FF2_W1, FF2_B1, ws.t, DFF, COHERE_EPI_SILU, DFF, 1.f), "feed-forward 2 W1");
+    RUN(gemm(ws.t, DFF, ly, FF2_W2, FF2_B2, x, DM, COHERE_EPI_RESID, DM, 0.5f), "feed-forward 2 W2");
+    if (i + 1 < n_layers) {
+      const void* const* nx = ly + N_FIELDS;
+      RUN(cohere_layernorm(x, DM, fld<uint16_t>(ly, LN_OUT_W), fld<uint16_t>(ly, LN_OUT_B), ep(i, EPS_OUT),
+                           fld<uint16_t>(nx, LN_FF1_W), fld<uint16_t>(nx, LN_FF1_B), ep(i + 1, EPS_FF1), ws.h, DM,
+                           rows, DM, stream),
+          "output LayerNorm");
+    } else {
+      RUN(cohere_layernorm(x, DM, fld<uint16_t>(ly, LN_OUT_W), fld<uint16_t>(ly, LN_OUT_B), ep(i, EPS_OUT), nullptr,
+                           nullptr, 0.f, x, DM, rows, DM, stream),
+          "output LayerNorm");
+    }
+  }
+#undef RUN
+  return 0;
+}
+
+}  // namespace
 
 extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers,
                                      const double* eps, const int32_t* tiles, int64_t n_tiles, const int32_t* lo,
@@ -80,7 +183,6 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
                                      double scale, int32_t heads, int32_t head_dim, int32_t int8, const int64_t* cfg,
                                      int64_t n_cfg, void* workspace, int64_t workspace_bytes, void* stream) {
   cohere::clear_error();
-  COHERE_REQUIRE(int8, "encoder_layers: only the int8 (W8A8) layers are provided; the bf16 branch is not");
   COHERE_REQUIRE(n_cfg >= 5, "encoder_layers: cfg needs at least 5 entries");
   COHERE_REQUIRE((int64_t)heads * head_dim == DM, "encoder_layers: heads x head size must be 1280");
   COHERE_REQUIRE(rows >= 0 && n_layers >= 0 && x && fields && eps, "encoder_layers: bad arguments");
@@ -89,21 +191,30 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
   const int64_t c_sp = n_cfg > 7 ? cfg[7] : 0;
   COHERE_REQUIRE(group > 0 && DFF % group == 0, "encoder_layers: the feed-forward group must divide 5120");
   if (rows == 0 || n_layers == 0) return 0;
+  const int64_t need = cohere_encoder_workspace_bytes(rows, group);
+  COHERE_REQUIRE(workspace && workspace_bytes >= need,
+                 "encoder_layers: workspace needs " + std::to_string(need) + " bytes");
+  if (!int8) {
+    COHERE_REQUIRE(cfg[0] == 3 || cfg[0] == 5 || cfg[0] == 8, "encoder_layers: unknown bf16 GEMM config");
+    return encoder_layers_bf16(x, rows, fields, n_layers, eps, tiles, n_tiles, lo, hi, rel_off, max_len, rel_rows,
+                               scale, heads, head_dim, cfg[0], carve_bf16(workspace, rows), stream);
+  }
   const Workspace ws = carve(workspace, rows, group);
-  COHERE_REQUIRE(workspace && workspace_bytes >= ws.bytes,
-                 "encoder_layers: workspace needs " + std::to_string(ws.bytes) + " bytes");
   // biases may be null (the GEMMs then skip them); the 2:4 and dense feed-forward W2 are alternatives
   static const int required[] = {LN_FF1_W, LN_FF1_B, LN_ATT_W, LN_ATT_B, LN_CONV_W, LN_CONV_B, LN_FF2_W, LN_FF2_B,
-                                 LN_OUT_W, LN_OUT_B, BU, BV, RK, WDW, BDW, BN_SCALE, BN_SHIFT, Q_FF1_W1, Q_FF1_S1,
-                                 Q_FF1_S2, Q_FF2_W1, Q_FF2_S1, Q_FF2_S2, Q_QKV_W, Q_QKV_S, Q_PW1_W, Q_PW1_S, Q_O_W,
+                                 LN_OUT_W, LN_OUT_B, BU, BV, RK, WDW, BDW, BN_SCALE, BN_SHIFT, Q_FF1_S1,
+                                 Q_FF1_S2, Q_FF2_S1, Q_FF2_S2, Q_QKV_W, Q_QKV_S, Q_PW1_W, Q_PW1_S, Q_O_W,
                                  Q_O_S, Q_PW2_W, Q_PW2_S};
   for (int64_t l = 0; l < n_layers; ++l) {
     const void* const* ly = fields + l * N_FIELDS;
     for (int f : required)
       COHERE_REQUIRE(ly[f], "encoder_layers: layer " + std::to_string(l) + " misses field " + std::to_string(f));
     COHERE_REQUIRE((ly[SP_FF1_W] ? ly[SP_FF1_E] != nullptr : ly[Q_FF1_W2] != nullptr) &&
-                       (ly[SP_FF2_W] ? ly[SP_FF2_E] != nullptr : ly[Q_FF2_W2] != nullptr),
-                   "encoder_layers: layer " + std::to_string(l) + ": a feed-forward W2 has neither dense nor 2:4 weights");
+                       (ly[SP_FF2_W] ? ly[SP_FF2_E] != nullptr : ly[Q_FF2_W2] != nullptr) &&
+                       (ly[SP_FF1_W1] ? ly[SP_FF1_E1] != nullptr : ly[Q_FF1_W1] != nullptr) &&
+                       (ly[SP_FF2_W1] ? ly[SP_FF2_E1] != nullptr : ly[Q_FF2_W1] != nullptr),
+                   "encoder_layers: layer " + std::to_string(l) +
+                       ": a feed-forward linear has neither dense nor 2:4 weights");
   }
 
   const int64_t ts_ld = DFF / group;
@@ -120,11 +231,25 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
   RUN(cohere_layernorm_q8(x, DM, fld<uint16_t>(l0, LN_FF1_W), fld<uint16_t>(l0, LN_FF1_B), ep(0, EPS_FF1), nullptr,
                           nullptr, 0.f, ws.hq, DM, ws.hs, rows, DM, stream),
       "first LayerNorm");
-  auto ffn = [&](const void* const* ly, int w1, int s1, int b1, int w2, int s2, int b2, int spw, int spe) {
-    RUN(cohere_gemm_i8(ws.hq, DM, ws.hs, 1, DM, fld<int8_t>(ly, w1), fld<float>(ly, s1), fld<uint16_t>(ly, b1),
-                       ws.tq, DFF, COHERE_EPI_SILU_Q8, nullptr, 0, 1.f, ws.ts, ts_ld, rows, DFF, DM, (int32_t)c_ff1,
-                       stream),
-        "feed-forward W1");
+  // the 2:4 SILU_Q8 GEMM writes one scale per row and 256 columns: the dense W1's output group must match it
+  COHERE_REQUIRE(group == 256 || [&] {
+    for (int64_t l = 0; l < n_layers; ++l)
+      if (fields[l * N_FIELDS + SP_FF1_W1] || fields[l * N_FIELDS + SP_FF2_W1]) return false;
+    return true;
+  }(), "encoder_layers: a 2:4 first feed-forward linear needs the feed-forward group 256");
+  auto ffn = [&](const void* const* ly, int w1, int s1, int b1, int w2, int s2, int b2, int spw, int spe, int spw1,
+                 int spe1) {
+    if (ly[spw1]) {
+      RUN(cohere_gemm_sp(ws.hq, DM, ws.hs, 1, DM, fld<int8_t>(ly, spw1), fld<int32_t>(ly, spe1), fld<float>(ly, s1),
+                         fld<uint16_t>(ly, b1), ws.tq, DFF, COHERE_EPI_SILU_Q8, nullptr, 0, 1.f, ws.ts, ts_ld, rows,
+                         DFF, DM, (int32_t)c_sp, stream),
+          "feed-forward W1 (2:4)");
+    } else {
+      RUN(cohere_gemm_i8(ws.hq, DM, ws.hs, 1, DM, fld<int8_t>(ly, w1), fld<float>(ly, s1), fld<uint16_t>(ly, b1),
+                         ws.tq, DFF, COHERE_EPI_SILU_Q8, nullptr, 0, 1.f, ws.ts, ts_ld, rows, DFF, DM,
+                         (int32_t)c_ff1, stream),
+          "feed-forward W1");
+    }
     if (ly[spw]) {
       RUN(cohere_gemm_sp(ws.tq, DFF, ws.ts, ts_ld, group, fld<int8_t>(ly, spw), fld<int32_t>(ly, spe),
                          fld<float>(ly, s2), fld<uint16_t>(ly, b2), x, DM, COHERE_EPI_RESID, x, DM, 0.5f, nullptr, 0,
@@ -140,7 +265,8 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
   };
   for (i = 0; i < n_layers; ++i) {
     const void* const* ly = fields + i * N_FIELDS;
-    if (ffn(ly, Q_FF1_W1, Q_FF1_S1, FF1_B1, Q_FF1_W2, Q_FF1_S2, FF1_B2, SP_FF1_W, SP_FF1_E)) return 1;
+    if (ffn(ly, Q_FF1_W1, Q_FF1_S1, FF1_B1, Q_FF1_W2, Q_FF1_S2, FF1_B2, SP_FF1_W, SP_FF1_E, SP_FF1_W1, SP_FF1_E1))
+      return 1;
     RUN(cohere_layernorm_q8(x, DM, fld<uint16_t>(ly, LN_ATT_W), fld<uint16_t>(ly, LN_ATT_B), ep(i, EPS_ATT), nullptr,
                             nullptr, 0.f, ws.hq, DM, ws.hs, rows, DM, stream),
         "attention LayerNorm");
@@ -175,7 +301,8 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
     RUN(cohere_layernorm_q8(x, DM, fld<uint16_t>(ly, LN_FF2_W), fld<uint16_t>(ly, LN_FF2_B), ep(i, EPS_FF2), nullptr,
                             nullptr, 0.f, ws.hq, DM, ws.hs, rows, DM, stream),
         "feed-forward 2 LayerNorm");
-    if (ffn(ly, Q_FF2_W1, Q_FF2_S1, FF2_B1, Q_FF2_W2, Q_FF2_S2, FF2_B2, SP_FF2_W, SP_FF2_E)) return 1;
+    if (ffn(ly, Q_FF2_W1, Q_FF2_S1, FF2_B1, Q_FF2_W2, Q_FF2_S2, FF2_B2, SP_FF2_W, SP_FF2_E, SP_FF2_W1, SP_FF2_E1))
+      return 1;
     if (i + 1 < n_layers) {
       const void* const* nx = ly + N_FIELDS;
       RUN(cohere_layernorm_q8(x, DM, fld<uint16_t>(ly, LN_OUT_W), fld<uint16_t>(ly, LN_OUT_B), ep(i, EPS_OUT),

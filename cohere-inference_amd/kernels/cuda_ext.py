@@ -93,6 +93,9 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+_EMPTY = torch.empty(0)  # an absent per-layer tensor
+
+
 def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
@@ -309,12 +312,14 @@ class _Ext:
     def encoder_layers(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
         """Every layer on packed frames x (N, 1280) bf16, in place, launched from native code
         (kernels/csrc/encoder_loop.cpp:50-99). layers: per layer the tensors in the reference's field order
-        (fast_encoder.py:121-130); empty tensors stand for absent ones. int8 must be True."""
-        _check(bool(int8), "encoder_layers: only the int8 (W8A8) layers are provided")
+        (fast_encoder.py:121-130), 53 of them, optionally followed by 4 more (the feed-forwards' first linears in
+        2:4 form: ff1 kept, ff1 selectors, ff2 kept, ff2 selectors); empty tensors stand for absent ones. int8: the
+        W8A8 branch on the quantized fields, else the bf16 branch on the bf16 weights (encoder_loop.cpp:101-124)."""
         _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.shape[1] == 1280,
                "encoder_layers: x (N, 1280) contiguous bf16")
-        n_fields = 53
-        _check(all(len(ly) == n_fields for ly in layers), f"encoder_layers: {n_fields} tensors per layer")
+        n_ref, n_fields = 53, 57
+        _check(all(len(ly) in (n_ref, n_fields) for ly in layers),
+               f"encoder_layers: {n_ref} or {n_fields} tensors per layer")
         _check(len(eps) == 5 * len(layers), "encoder_layers: 5 epsilons per layer")
         for ly in layers:
             for t in ly:
@@ -326,15 +331,16 @@ class _Ext:
             return
         H, D = layers[0][22].shape  # bias_u: (heads, head size)
         ptrs = (ctypes.c_void_p * (n_fields * len(layers)))(
-            *[t.data_ptr() if t.numel() > 0 else None for ly in layers for t in ly])
+            *[t.data_ptr() if t.numel() > 0 else None for ly in layers
+              for t in (*ly, *([_EMPTY] * (n_fields - len(ly))))])
         eps_arr = (ctypes.c_double * len(eps))(*[float(e) for e in eps])
         cfg_arr = (ctypes.c_int64 * len(cfg))(*cfg)
         nbytes = self.encoder_workspace_bytes(rows, cfg[4])
         _check(nbytes >= 0, "encoder_layers: bad feed-forward group")
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         self._call("cohere_encoder_layers", _ptr(x), rows, ptrs, len(layers), eps_arr, _ptr(tiles), tiles.shape[0],
-                   _ptr(lo), _ptr(hi), int(rel_off), int(max_len), layers[0][24].shape[0], float(scale), H, D, 1,
-                   cfg_arr, len(cfg), _ptr(ws), nbytes, _stream())
+                   _ptr(lo), _ptr(hi), int(rel_off), int(max_len), layers[0][24].shape[0], float(scale), H, D,
+                   int(bool(int8)), cfg_arr, len(cfg), _ptr(ws), nbytes, _stream())
 
     # ---- decoder projections (bindings.cpp:55-56) -----------------------------------------------------------
 

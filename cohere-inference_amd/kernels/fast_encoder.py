@@ -105,7 +105,9 @@ LAYER_FIELDS = (
     "ln_out_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2", "wqkv", "bqkv", "wo",
     "bo", "bu", "bv", "rk", "wpw1", "bpw1", "wdw", "bdw", "bn_scale", "bn_shift", "wpw2", "bpw2", "q_ff1_w1",
     "q_ff1_s1", "q_ff1_w2", "q_ff1_s2", "q_ff2_w1", "q_ff2_s1", "q_ff2_w2", "q_ff2_s2", "q_qkv_w", "q_qkv_s",
-    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e")
+    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e",
+    # this build's own: the feed-forwards' first linears in 2:4 form (the reference keeps them dense)
+    "sp_ff1_w1", "sp_ff1_e1", "sp_ff2_w1", "sp_ff2_e1")
 GEMM_CFG = 8  # the reference's bf16 GEMM config id (its first cfg entry; unused on the int8 path)
 MAX_LEN = 512  # encoder frames the distance table covers (reference fast_encoder.py:135)
 
@@ -122,54 +124,70 @@ def relative_table(inv_freq: torch.Tensor, relative_k_proj_weight: torch.Tensor,
 
 
 class EncoderLayer:
-    """One FastConformer block's tensors for the int8 layer loop (reference fast_encoder.py:66-131, int8 only): every
+    """One FastConformer block's tensors for the native layer loop (reference fast_encoder.py:66-131). int8: every
     linear W8A8 per output channel; with sparse, the feed-forwards' second linears pruned 2:4 by magnitude (a no-op on
-    weights that already are) before quantization and stored compressed, their dense form dropped."""
+    weights that already are) before quantization and stored compressed, their dense form dropped; sparse_w1 does the
+    same to the feed-forwards' first linears (both feed-forward linears 2:4; the reference prunes only the second).
+    Without int8 the linears keep their bf16 weights (the reference's INT8=0 layers)."""
 
-    def __init__(self, blk, rk: torch.Tensor, sparse: bool = False):
+    def __init__(self, blk, rk: torch.Tensor, sparse: bool = False, sparse_w1: bool = False, int8: bool = True):
+        if (sparse or sparse_w1) and not int8:
+            raise ValueError("EncoderLayer: the 2:4 linears are int8 only")
         t = {}
-        ln = lambda m: (m.weight.contiguous(), m.bias.contiguous(), m.eps)  # noqa: E731
         lns = (blk.norm_feed_forward1, blk.norm_self_att, blk.norm_conv, blk.norm_feed_forward2, blk.norm_out)
         self.eps = []
         for name, m in zip(("ff1", "att", "conv", "ff2", "out"), lns):
-            t[f"ln_{name}_w"], t[f"ln_{name}_b"], e = ln(m)
-            self.eps.append(float(e))
-        empty_bf = torch.empty(0, device=rk.device, dtype=rk.dtype)
-        empty_i8 = torch.empty(0, device=rk.device, dtype=torch.int8)
+            t[f"ln_{name}_w"], t[f"ln_{name}_b"] = m.weight.contiguous(), m.bias.contiguous()
+            self.eps.append(float(m.eps))
+        dev = rk.device
+        none_bf = torch.empty(0, device=dev, dtype=rk.dtype)
+        none_i8 = torch.empty(0, device=dev, dtype=torch.int8)
+        none_f32 = torch.empty(0, device=dev, dtype=torch.float32)
+        none_i32 = torch.empty(0, device=dev, dtype=torch.int32)
         at, cv = blk.self_attn, blk.conv
         c = cv.depthwise_conv.in_channels
-        w1, b1 = cv.pointwise_conv1.weight[:, :, 0], cv.pointwise_conv1.bias
-        wpw1 = torch.stack([w1[:c], w1[c:]], 1).reshape(2 * c, -1)  # GLU halves interleaved (a_0, g_0, a_1, ...)
-        bpw1 = torch.stack([b1[:c], b1[c:]], 1).reshape(2 * c)
-        bn = cv.norm
-        scale = bn.weight.float() / torch.sqrt(bn.running_var.float() + bn.eps)
-        for k, ff in (("ff1", blk.feed_forward1), ("ff2", blk.feed_forward2)):
-            t[f"{k}_w1"], t[f"{k}_w2"] = empty_bf, empty_bf
-            t[f"{k}_b1"], t[f"{k}_b2"] = ff.linear1.bias.contiguous(), ff.linear2.bias.contiguous()
-            t[f"q_{k}_w1"], t[f"q_{k}_s1"] = quantize_rows(ff.linear1.weight)
-            w2 = prune_24_magnitude(ff.linear2.weight) if sparse else ff.linear2.weight
-            t[f"q_{k}_w2"], t[f"q_{k}_s2"] = quantize_rows(w2)
-            if sparse:
-                t[f"sp_{k}_w"], t[f"sp_{k}_e"] = compress_24(t[f"q_{k}_w2"])
-                t[f"q_{k}_w2"] = empty_i8
-            else:
-                t[f"sp_{k}_w"], t[f"sp_{k}_e"] = empty_i8, empty_i8.int()
-        wqkv = torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight])
+        pw1, pb1 = cv.pointwise_conv1.weight[:, :, 0], cv.pointwise_conv1.bias
+        # the GLU's value and gate rows interleaved (a_0, g_0, a_1, g_1, ...): one epilogue lane sees both
+        linears = {"ff1_w1": blk.feed_forward1.linear1.weight, "ff1_w2": blk.feed_forward1.linear2.weight,
+                   "ff2_w1": blk.feed_forward2.linear1.weight, "ff2_w2": blk.feed_forward2.linear2.weight,
+                   "wqkv": torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight]),
+                   "wo": at.o_proj.weight, "wpw1": torch.stack([pw1[:c], pw1[c:]], 1).reshape(2 * c, -1),
+                   "wpw2": cv.pointwise_conv2.weight[:, :, 0]}
+        t["ff1_b1"], t["ff1_b2"] = blk.feed_forward1.linear1.bias.contiguous(), blk.feed_forward1.linear2.bias.contiguous()
+        t["ff2_b1"], t["ff2_b2"] = blk.feed_forward2.linear1.bias.contiguous(), blk.feed_forward2.linear2.bias.contiguous()
         t["bqkv"] = torch.cat([at.q_proj.bias, at.k_proj.bias, at.v_proj.bias]).contiguous()
-        t["wqkv"] = t["wo"] = t["wpw1"] = t["wpw2"] = empty_bf
         t["bo"], t["bu"], t["bv"], t["rk"] = (at.o_proj.bias.contiguous(), at.bias_u.contiguous(),
                                               at.bias_v.contiguous(), rk)
-        t["bpw1"] = bpw1.contiguous()
+        t["bpw1"] = torch.stack([pb1[:c], pb1[c:]], 1).reshape(2 * c).contiguous()
+        t["bpw2"] = cv.pointwise_conv2.bias.contiguous()
         t["wdw"] = cv.depthwise_conv.weight[:, 0, :].float().contiguous()
         t["bdw"] = cv.depthwise_conv.bias.float().contiguous()
-        t["bn_scale"] = scale.contiguous()
-        t["bn_shift"] = (bn.bias.float() - bn.running_mean.float() * scale).contiguous()
-        t["bpw2"] = cv.pointwise_conv2.bias.contiguous()
-        t["q_qkv_w"], t["q_qkv_s"] = quantize_rows(wqkv)
-        t["q_pw1_w"], t["q_pw1_s"] = quantize_rows(wpw1)
-        t["q_o_w"], t["q_o_s"] = quantize_rows(at.o_proj.weight)
-        t["q_pw2_w"], t["q_pw2_s"] = quantize_rows(cv.pointwise_conv2.weight[:, :, 0])
+        bn = cv.norm
+        bn_scale = bn.weight.float() / torch.sqrt(bn.running_var.float() + bn.eps)
+        t["bn_scale"] = bn_scale.contiguous()
+        t["bn_shift"] = (bn.bias.float() - bn.running_mean.float() * bn_scale).contiguous()
+        # quantized names of each linear: (int8 weight, scale) fields and, for the feed-forwards, the 2:4 pair
+        qnames = {"ff1_w1": ("q_ff1_w1", "q_ff1_s1", "sp_ff1_w1", "sp_ff1_e1"),
+                  "ff1_w2": ("q_ff1_w2", "q_ff1_s2", "sp_ff1_w", "sp_ff1_e"),
+                  "ff2_w1": ("q_ff2_w1", "q_ff2_s1", "sp_ff2_w1", "sp_ff2_e1"),
+                  "ff2_w2": ("q_ff2_w2", "q_ff2_s2", "sp_ff2_w", "sp_ff2_e"),
+                  "wqkv": ("q_qkv_w", "q_qkv_s"), "wo": ("q_o_w", "q_o_s"), "wpw1": ("q_pw1_w", "q_pw1_s"),
+                  "wpw2": ("q_pw2_w", "q_pw2_s")}
+        for name, w in linears.items():
+            q = qnames[name]
+            for k, empty in zip(q, (none_i8, none_f32, none_i8, none_i32)):
+                t[k] = empty
+            if not int8:
+                t[name] = w.contiguous()
+                continue
+            t[name] = none_bf
+            pruned = len(q) == 4 and (sparse if name.endswith("w2") else sparse_w1)
+            t[q[0]], t[q[1]] = quantize_rows(prune_24_magnitude(w) if pruned else w)
+            if pruned:
+                t[q[2]], t[q[3]] = compress_24(t[q[0]])
+                t[q[0]] = none_i8
         self.tensors = t
+        self.int8 = int8
         self.heads, self.head_dim = at.bias_u.shape
 
     def fields(self) -> list[torch.Tensor]:
@@ -192,14 +210,17 @@ def metadata(lengths: list[int], device) -> dict:
 
 
 class EncoderLayers:
-    """The int8 layers of a FastConformer encoder on packed frames (reference FastEncoder.layers_forward,
+    """The layers of a FastConformer encoder on packed frames (reference FastEncoder.layers_forward,
     fast_encoder.py:215-226): blocks are transformers ParakeetEncoderBlock modules (1280 wide, 8 or 16 heads) whose
-    weights are converted once; a call runs every layer through ext.encoder_layers, one native launch loop."""
+    weights are converted once; a call runs every layer through ext.encoder_layers, one native launch loop. sparse /
+    sparse_w1 / int8 as EncoderLayer."""
 
-    def __init__(self, blocks, inv_freq: torch.Tensor, sparse: bool = False, max_len: int = MAX_LEN):
+    def __init__(self, blocks, inv_freq: torch.Tensor, sparse: bool = False, max_len: int = MAX_LEN,
+                 sparse_w1: bool = False, int8: bool = True):
         with torch.no_grad():
             self.layers = [EncoderLayer(b, relative_table(inv_freq, b.self_attn.relative_k_proj.weight, max_len),
-                                        sparse) for b in blocks]
+                                        sparse, sparse_w1, int8) for b in blocks]
+        self.int8 = int8
         self.layer_tensors = [ly.fields() for ly in self.layers]
         self.layer_eps = [e for ly in self.layers for e in ly.eps]
         self.max_len, self.rel_off = max_len, max_len - 1
@@ -217,22 +238,23 @@ class EncoderLayers:
         if meta["max_len"] > self.max_len:
             raise RuntimeError(f"encoder_layers: sequence of {meta['max_len']} frames exceeds {self.max_len}")
         ext.encoder_layers(x, self.layer_tensors, self.layer_eps, meta["tiles"], meta["lo"], meta["hi"], self.rel_off,
-                           meta["max_len"], self.scale, True, self.configs(x.shape[0]))
+                           meta["max_len"], self.scale, self.int8, self.configs(x.shape[0]))
         return x
 
 
 class FastEncoder:
     """A transformers ParakeetEncoder (bf16, on the GPU) on packed pieces (reference fast_encoder.py:133-232): the
     subsampling stem per piece without padding (sub_conv0_dw, the pointwise convolutions and final linear as bf16
-    GEMMs, sub_dw), then the int8 layer loop. int8 must be true (the reference's bf16 layer branch is not provided).
-    sparse: a file of 2:4-pruned second feed-forward weights (as the reference), or True to prune them by magnitude
-    here; None keeps every layer dense."""
+    GEMMs, sub_dw), then the native layer loop: W8A8 with int8, else bf16 (the reference's default). sparse (int8
+    only): a file of 2:4-pruned second feed-forward weights (as the reference), or True to prune them by magnitude
+    here; None keeps every layer dense. sparse_w1 prunes the feed-forwards' first linears 2:4 by magnitude as well
+    (this build's option: every feed-forward linear 2:4)."""
 
     MAX_LEN = MAX_LEN
 
-    def __init__(self, encoder, int8: bool = True, sparse: str | bool | None = None):
-        if not int8:
-            raise ValueError("FastEncoder: only the int8 layers are provided")
+    def __init__(self, encoder, int8: bool = False, sparse: str | bool | None = None, sparse_w1: bool = False):
+        if (sparse is not None and sparse is not False or sparse_w1) and not int8:
+            raise ValueError("FastEncoder: the 2:4 feed-forwards need int8")
         cfg = encoder.config
         if cfg.hidden_size != 1280 or getattr(cfg, "scale_input", False):
             raise ValueError("FastEncoder: 1280-wide encoders without input scaling only")
@@ -249,7 +271,7 @@ class FastEncoder:
                 raise ValueError("FastEncoder: the file must prune every feed-forward's second layer")
         self.encoder, self.int8, self.sparse = encoder, int8, sparse is not None and sparse is not False
         self.layers = EncoderLayers(encoder.layers, encoder.encode_positions.inv_freq, sparse=self.sparse,
-                                    max_len=self.MAX_LEN)
+                                    max_len=self.MAX_LEN, sparse_w1=sparse_w1, int8=int8)
         with torch.no_grad():
             # subsampling: [conv0, ReLU, dw, pw, ReLU, dw, pw, ReLU] + linear; the linear's input columns reordered
             # from (channel, frequency) to the channels-last (frequency, channel)

@@ -83,56 +83,83 @@ def default_extractor():
                                  dither=1e-5, mel_filters=slaney_mel_filters())
 
 
+class _Staging:
+    """Pinned host buffers for the samples of numpy pieces, used in turn (two, so that one call's upload can still be
+    in flight while the next call fills the other); each is reused only after the upload that last read it."""
+
+    def __init__(self, count: int = 2):
+        self.slots = [[torch.empty(0, dtype=torch.float32).pin_memory(), None] for _ in range(count)]
+        self.turn = 0
+
+    def upload(self, pieces: list, total: int, device) -> torch.Tensor:
+        slot = self.slots[self.turn]
+        self.turn = (self.turn + 1) % len(self.slots)
+        if slot[1] is not None:
+            slot[1].synchronize()
+        if slot[0].numel() < total:
+            slot[0] = torch.empty(max(total, 2 * slot[0].numel()), dtype=torch.float32).pin_memory()
+        host = slot[0][:total].numpy()
+        at = 0
+        for p in pieces:
+            n = len(p)
+            host[at:at + n] = np.asarray(p, dtype=np.float32)
+            at += n
+        dev = slot[0][:total].to(device, non_blocking=True)
+        slot[1] = torch.cuda.Event()
+        slot[1].record()
+        return dev
+
+
 class Features:
-    """Reference kernels/features.py:41-88 (Features): the extractor's window, filter bank and their nonzero bands
-    prepared once; a call computes every piece's features with one native call."""
+    """Normalised log-mel features of a batch of pieces (reference kernels/features.py:41-88, same call surface):
+    the extractor's Hann window (centred in the 512-point frame) and filter bank are prepared once, with each mel
+    band's first and end nonzero bins, in the layout the log-mel kernel reads; a call is one native launch sequence
+    over the valid frames of every piece."""
 
     def __init__(self, extractor=None, device="cuda"):
         fe = default_extractor() if extractor is None else extractor
-        if not (fe.n_fft == 512 and fe.hop_length == 160 and fe.win_length == 400):
+        if (fe.n_fft, fe.hop_length, fe.win_length) != (512, 160, 400):
             raise ValueError("Features: the kernels take n_fft 512, hop 160, window 400")
         self.n_fft, self.hop, self.win = fe.n_fft, fe.hop_length, fe.win_length
-        self.preemphasis = fe.preemphasis
+        self.preemphasis = float(fe.preemphasis)
         self.device = torch.device(device)
-        self.window = torch.hann_window(self.win, periodic=False, device=self.device)
-        self.mel = fe.mel_filters.to(self.device, torch.float32).contiguous()  # (128, 257)
-        self.mels = self.mel.shape[0]
-        if self.mel.shape != (128, 257):
+        mel = torch.as_tensor(fe.mel_filters, dtype=torch.float32).cpu()
+        if tuple(mel.shape) != (128, 257):
             raise ValueError("Features: the kernels take 128 mel bands over 257 bins")
-        left = (self.n_fft - self.win) // 2  # torch.stft centres the window in n_fft
-        self.window512 = torch.zeros(self.n_fft, device=self.device)
-        self.window512[left:left + self.win] = self.window
-        nz = (self.mel != 0).cpu()
-        first = nz.int().argmax(1)
-        end = self.mel.shape[1] - nz.flip(1).int().argmax(1)
-        self.band = torch.stack([first, torch.where(nz.any(1), end, first)], 1).int().contiguous().to(self.device)
-        self.pinned = torch.empty(0, dtype=torch.float32).pin_memory()  # the samples' staging buffer, grown as needed
-        self.copied = None  # event: the last copy out of it
+        self.mels = mel.shape[0]
+        self.mel = mel.contiguous().to(self.device)
+        # torch.stft places the 400-point window in the middle of the 512-point frame
+        self.window = torch.hann_window(self.win, periodic=False)
+        frame_window = torch.zeros(self.n_fft)
+        first = (self.n_fft - self.win) // 2
+        frame_window[first:first + self.win] = self.window
+        self.window512 = frame_window.to(self.device)
+        self.window = self.window.to(self.device)
+        edges = []
+        for row in mel.numpy():
+            nz = np.flatnonzero(row)
+            edges.append((nz[0], nz[-1] + 1) if nz.size else (0, 0))
+        self.band = torch.tensor(edges, dtype=torch.int32).to(self.device)
+        self._staging = _Staging()
 
     @torch.no_grad()
     def __call__(self, pieces: list) -> tuple[torch.Tensor, list[int]]:
-        """Normalised log-mel frames (B, T, 128) bf16 of dithered pieces (numpy arrays, or fp32 tensors already on
-        the GPU), zero past each piece's frames, and the frame counts (n // 160 + 1)."""
-        lengths = [len(p) for p in pieces]
-        total = sum(lengths)
+        """(B, T, 128) bf16 normalised log-mel frames of dithered pieces (numpy arrays, or fp32 tensors on the GPU),
+        zero past each piece's frames, and the frame counts: a piece of n samples has n // 160 + 1 frames, the last
+        one zero, as the service always fed the model."""
+        sizes = [len(p) for p in pieces]
         if all(isinstance(p, torch.Tensor) for p in pieces):
-            flat = torch.cat([p.reshape(-1).to(self.device, torch.float32) for p in pieces])
+            samples = torch.cat([p.reshape(-1).to(self.device, torch.float32) for p in pieces])
         else:
-            if self.copied is not None:
-                self.copied.synchronize()  # the previous call's samples are out of the staging buffer
-            if self.pinned.numel() < total:
-                self.pinned = torch.empty(max(total, 2 * self.pinned.numel()), dtype=torch.float32).pin_memory()
-            np.concatenate([np.asarray(p, dtype=np.float32) for p in pieces], out=self.pinned[:total].numpy())
-            flat = self.pinned[:total].to(self.device, non_blocking=True)
-            self.copied = torch.cuda.Event()
-            self.copied.record()
-        valid = [n // self.hop for n in lengths]
-        meta = torch.tensor(np.concatenate([np.cumsum([0] + lengths[:-1]), lengths, np.cumsum([0] + valid)]),
-                            dtype=torch.int64).to(self.device, non_blocking=True)
-        out = torch.zeros(len(pieces), max(lengths) // self.hop + 1, self.mels, device=self.device,
+            samples = self._staging.upload(pieces, sum(sizes), self.device)
+        valid = np.asarray(sizes, dtype=np.int64) // self.hop
+        meta = np.concatenate([np.cumsum([0] + sizes[:-1]), sizes, np.concatenate([[0], np.cumsum(valid)])])
+        meta = torch.from_numpy(meta.astype(np.int64)).pin_memory().to(self.device, non_blocking=True)
+        out = torch.zeros(len(pieces), max(sizes) // self.hop + 1, self.mels, device=self.device,
                           dtype=torch.bfloat16)
-        ext.logmel_features(flat, meta, sum(valid), self.window512, self.mel, self.band, self.preemphasis, out)
-        return out, [n + 1 for n in valid]
+        ext.logmel_features(samples, meta, int(valid.sum()), self.window512, self.mel, self.band, self.preemphasis,
+                            out)
+        return out, [int(v) + 1 for v in valid]
 
 
 __all__ = ["EPS", "LOG_GUARD", "Features", "default_extractor", "dither", "slaney_mel_filters"]

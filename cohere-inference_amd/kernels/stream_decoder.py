@@ -1,8 +1,9 @@
-"""Greedy decoding with continuous batching on gfx950 (the reference's kernels/stream_decoder.py): the int8-weight
-(W8A16) layout and 64-row chunked projection calls (prepare_w8 38-48, W8_CONFIGS 30-35, _w8 148-158) over the skinny
-HIP GEMMs of csrc/dec_w8.hip, and the StreamDecoder itself (73-276): per-slot state and KV caches, one step = embedding,
-8 x (self-attention over the slot's int8 cache, cross-attention, feed-forward), head and greedy pick, captured into one
-HIP graph per bucket of row counts (csrc/decoder_ops.hip for the non-GEMM kernels).
+"""Greedy decoding with continuous batching on gfx950 (the call surface of the reference's kernels/stream_decoder.py):
+the int8-weight (W8A16) layout and 64-row chunked projection calls (prepare_w8 38-48, W8_CONFIGS 30-35, _w8 148-158)
+over the skinny HIP GEMMs of csrc/dec_w8.hip, and StreamDecoder (73-276): per-slot state and KV caches, one step =
+embedding, 8 x (self-attention over the slot's int8 cache, cross-attention, feed-forward), head and greedy pick, held
+as a fixed list of launches over preallocated buffers and captured into one HIP graph per bucket of row counts
+(csrc/decoder_ops.hip for the non-GEMM kernels).
 
     wq = prepare_w8(w_bf16)                          # (uint8 (N, K), fp32 (N))
     y = w8_linear(x, wq, bias, relu=False, ws=ws, counters=counters)
@@ -84,31 +85,62 @@ def bf16_linear(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None, relu: 
     return y
 
 
-# ---- the step and its graphs (reference stream_decoder.py:60-276) ----------------------------------------------------
+# ---- the decoder and its captured step ------------------------------------------------------------------------------
 
-class _Layer:
-    """One decoder layer's tensors (reference stream_decoder.py:60-71)."""
+class _Projection:
+    """One decoder linear bound to its skinny kernel: int8 weights in prepare_w8's layout through dec_w8_linear, or
+    bf16 weights through linear_bf16. A call writes y (rows, N) from x (rows, K), 64 rows per launch."""
 
-    def __init__(self, layer):
-        sa, ca = layer.self_attn, layer.encoder_attn
-        ln = lambda m: (m.weight, m.bias, m.eps)  # noqa: E731
-        self.ln1, self.ln2, self.ln3 = ln(layer.input_layernorm), ln(layer.post_attention_layernorm), \
-            ln(layer.final_layernorm)
-        self.qkv = (torch.cat([sa.q_proj.weight, sa.k_proj.weight, sa.v_proj.weight]).contiguous(),
-                    torch.cat([sa.q_proj.bias, sa.k_proj.bias, sa.v_proj.bias]).contiguous())
-        self.o = (sa.o_proj.weight, sa.o_proj.bias)
-        self.cq = (ca.q_proj.weight, ca.q_proj.bias)
-        self.co = (ca.o_proj.weight, ca.o_proj.bias)
-        self.fc1 = (layer.mlp.fc1.weight, layer.mlp.fc1.bias)
-        self.fc2 = (layer.mlp.fc2.weight, layer.mlp.fc2.bias)
+    def __init__(self, weight: torch.Tensor, bias: torch.Tensor | None, int8: bool):
+        self.n, self.k = weight.shape
+        self.bias = None if bias is None else bias.contiguous()
+        if int8:
+            self.weight, self.scale = prepare_w8(weight)
+        else:
+            self.weight, self.scale = weight.contiguous(), None
+
+    @property
+    def nbytes(self) -> int:
+        return self.weight.numel() * self.weight.element_size()
+
+    def __call__(self, x: torch.Tensor, y: torch.Tensor, relu: bool = False) -> None:
+        for r in range(0, x.shape[0], 64):
+            xr, yr = x[r:r + 64], y[r:r + 64]
+            if self.scale is None:
+                ext.linear_bf16(xr, self.weight, self.bias, yr, relu)
+            else:
+                bn, _ = w8_config(self.n, self.k, xr.shape[0])
+                ext.dec_w8_linear(xr, self.weight, self.scale, self.bias, yr, relu, bn, 1, None, None)
+
+
+class _Block:
+    """One decoder layer: its three LayerNorms (weight, bias, eps) and six projections. With int8, the
+    self-attention's fused q/k/v and the feed-forward's two linears hold int8 weights; the attention outputs and the
+    cross-attention query stay bf16 (the reference's int8 layout, stream_decoder.py:106-113)."""
+
+    def __init__(self, layer, int8: bool):
+        sa, ca, mlp = layer.self_attn, layer.encoder_attn, layer.mlp
+        self.norms = tuple((m.weight, m.bias, float(m.eps)) for m in
+                           (layer.input_layernorm, layer.post_attention_layernorm, layer.final_layernorm))
+        self.qkv = _Projection(torch.cat([sa.q_proj.weight, sa.k_proj.weight, sa.v_proj.weight]),
+                               torch.cat([sa.q_proj.bias, sa.k_proj.bias, sa.v_proj.bias]), int8)
+        self.o = _Projection(sa.o_proj.weight, sa.o_proj.bias, False)
+        self.cq = _Projection(ca.q_proj.weight, ca.q_proj.bias, False)
+        self.co = _Projection(ca.o_proj.weight, ca.o_proj.bias, False)
+        self.fc1 = _Projection(mlp.fc1.weight, mlp.fc1.bias, int8)
+        self.fc2 = _Projection(mlp.fc2.weight, mlp.fc2.bias, int8)
+
+    def projections(self):
+        return (self.qkv, self.o, self.cq, self.co, self.fc1, self.fc2)
 
 
 class StreamDecoder:
-    """Greedy decoding with continuous batching over per-slot state and KV caches, one HIP graph per bucket of row
-    counts (reference kernels/stream_decoder.py:73-276, same attributes and methods). The model is a transformers
-    CohereAsrForConditionalGeneration (or anything with its decoder attributes). Differences: the decoder stream has
-    the default priority (stream priorities are not used on this platform), and `frames` may be given instead of
-    asking the encoder for its subsampled length."""
+    """Greedy decoding with continuous batching (reference kernels/stream_decoder.py, same constructor, attributes
+    and methods). State lives in `slots` slots plus one dummy slot that padding rows point at; a step feeds one token
+    per active row. The step is a fixed list of launches over buffers allocated once (no allocation inside a step),
+    built per bucket of row counts and captured into one HIP graph per bucket, so a step is one graph replay whatever
+    the rows' positions and audio lengths. The model is a transformers CohereAsrForConditionalGeneration (or anything
+    with its decoder attributes); `frames` may be given instead of asking the encoder for its subsampled length."""
 
     BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96, 112, 128)
 
@@ -116,202 +148,250 @@ class StreamDecoder:
                  max_audio_s: float = 36.0, buckets=None, int8: bool = False, frames: int | None = None,
                  capture: bool = True):
         dec, cfg = model.model.decoder, model.config
-        self.buckets = tuple(b for b in (buckets or self.BUCKETS) if b <= slots)
-        self.model, self.max_new_tokens = model, max_new_tokens
-        self.h, self.d, self.width = cfg.num_attention_heads, getattr(cfg, "head_dim", None), cfg.hidden_size
-        self.d = self.d or self.width // self.h
-        assert self.d == 128, "the decoder kernels take head size 128"
-        self.eos, self.pad = cfg.eos_token_id, cfg.pad_token_id
-        self.scale = self.d ** -0.5
-        self.embed, self.pos_table = dec.embed_tokens.weight, dec.pos_emb.weight
-        ln = lambda m: (m.weight, m.bias, m.eps)  # noqa: E731
-        self.emb_ln, self.final_ln = ln(dec.embedding_layernorm), ln(dec.norm)
-        self.head = (model.proj_out.weight, model.proj_out.bias)
-        self.proj = (dec.proj.weight, dec.proj.bias)
-        self.layers = [_Layer(layer) for layer in dec.layers]
-        self.int8 = int8
-        if int8:
-            for ly in self.layers:
-                ly.qkv_w8, ly.fc1_w8, ly.fc2_w8 = prepare_w8(ly.qkv[0]), prepare_w8(ly.fc1[0]), prepare_w8(ly.fc2[0])
-            self.head_w8 = prepare_w8(self.head[0])
-        self.cross_w = torch.cat([w for layer in dec.layers for w in (layer.encoder_attn.k_proj.weight,
-                                                                       layer.encoder_attn.v_proj.weight)]).contiguous()
-        self.cross_b = torch.cat([b for layer in dec.layers for b in (layer.encoder_attn.k_proj.bias,
-                                                                       layer.encoder_attn.v_proj.bias)]).contiguous()
-        L, S = len(self.layers), slots
-        self.slots, self.dummy = S, S
-        self.max_prompt = max_prompt
-        self.seq = max_prompt + max_new_tokens + 1
+        self.model, self.int8 = model, int8
+        self.buckets = tuple(sorted(b for b in (buckets or self.BUCKETS) if b <= slots))
+        if not self.buckets:
+            raise ValueError("StreamDecoder: no bucket fits the slots")
+        self.h, self.width = cfg.num_attention_heads, cfg.hidden_size
+        self.d = getattr(cfg, "head_dim", None) or self.width // self.h
+        if self.d != 128:
+            raise ValueError("StreamDecoder: the decoder kernels take head size 128")
+        self.eos, self.pad, self.scale = cfg.eos_token_id, cfg.pad_token_id, self.d ** -0.5
+        self.slots, self.dummy = slots, slots
+        self.max_new_tokens, self.max_prompt = max_new_tokens, max_prompt
+        self.seq = max_prompt + max_new_tokens + 1  # cache positions per slot
         if frames is None:
             frames = int(model.model.encoder._get_subsampling_output_length(
                 torch.tensor([int(max_audio_s * 100) + 1])).item())
         self.frames = frames
-        dev, dt = self.embed.device, self.embed.dtype
-        self.device = dev
-        kv_dt = torch.int8 if int8 else dt
-        self.self_k = torch.zeros(L, S + 1, self.h, self.seq, self.d, device=dev, dtype=kv_dt)
-        self.self_v = torch.zeros_like(self.self_k)
-        self.cross_k = torch.zeros(L, S + 1, self.h, self.frames, self.d, device=dev, dtype=kv_dt)
-        self.cross_v = torch.zeros_like(self.cross_k)
-        if int8:  # one fp32 scale per 128-vector
-            self.self_ks = torch.ones(L, S + 1, self.h, self.seq, device=dev, dtype=torch.float32)
-            self.self_vs = torch.ones_like(self.self_ks)
-            self.cross_ks = torch.ones(L, S + 1, self.h, self.frames, device=dev, dtype=torch.float32)
-            self.cross_vs = torch.ones_like(self.cross_ks)
-        i32 = dict(device=dev, dtype=torch.int32)
-        self.cross_len = torch.ones(S + 1, **i32)
-        self.tok = torch.full((S + 1,), self.pad, device=dev, dtype=torch.long)
-        self.pos = torch.zeros(S + 1, **i32)
-        self.plen = torch.ones(S + 1, **i32)
-        self.limit = torch.zeros(S + 1, **i32)
-        self.finished = torch.ones(S + 1, device=dev, dtype=torch.uint8)
-        self.forced = torch.full((S + 1, max_prompt), self.pad, device=dev, dtype=torch.long)
-        self.out = torch.full((S + 1, self.seq + 1), self.pad, device=dev, dtype=torch.long)
-        self.active = torch.full((max(self.buckets),), S, **i32)
-        bm = max(self.buckets)
-        self.x = torch.zeros(bm, self.width, device=dev, dtype=dt)
-        self.hn = torch.zeros(bm, self.width, device=dev, dtype=dt)
-        self.att = torch.zeros(bm, self.width, device=dev, dtype=dt)
-        self.logits = torch.zeros(bm, self.head[0].shape[0], device=dev, dtype=dt)
+
+        # weights
+        self.embed, self.pos_table = dec.embed_tokens.weight, dec.pos_emb.weight
+        self.device = dev = self.embed.device
+        self.emb_ln = (dec.embedding_layernorm.weight, dec.embedding_layernorm.bias, float(dec.embedding_layernorm.eps))
+        self.final_ln = (dec.norm.weight, dec.norm.bias, float(dec.norm.eps))
+        self.blocks = [_Block(layer, int8) for layer in dec.layers]
+        self.layers = self.blocks
+        self.head = _Projection(model.proj_out.weight, model.proj_out.bias, int8)
+        self.proj = (dec.proj.weight.contiguous(), None if dec.proj.bias is None else dec.proj.bias.contiguous())
+        kv_w = [w for layer in dec.layers for w in (layer.encoder_attn.k_proj.weight, layer.encoder_attn.v_proj.weight)]
+        kv_b = [b for layer in dec.layers for b in (layer.encoder_attn.k_proj.bias, layer.encoder_attn.v_proj.bias)]
+        self.cross_w, self.cross_b = torch.cat(kv_w).contiguous(), torch.cat(kv_b).contiguous()
+
+        # caches: (layer, slot, head, position, 128), int8 with one fp32 scale per 128-vector when int8
+        L, S1 = len(self.blocks), slots + 1
+        kv_dtype = torch.int8 if int8 else self.embed.dtype
+
+        def cache(t):
+            return torch.zeros(L, S1, self.h, t, self.d, device=dev, dtype=kv_dtype)
+
+        def scales(t):
+            return torch.ones(L, S1, self.h, t, device=dev, dtype=torch.float32) if int8 else None
+
+        self.self_k, self.self_v, self.self_ks, self.self_vs = cache(self.seq), cache(self.seq), scales(self.seq), \
+            scales(self.seq)
+        self.cross_k, self.cross_v, self.cross_ks, self.cross_vs = cache(frames), cache(frames), scales(frames), \
+            scales(frames)
+
+        # slot state (row `slots` is the dummy, never advanced)
+        i32, i64 = dict(device=dev, dtype=torch.int32), dict(device=dev, dtype=torch.long)
+        self.tok = torch.full((S1,), self.pad, **i64)
+        self.pos = torch.zeros(S1, **i32)
+        self.plen = torch.ones(S1, **i32)
+        self.limit = torch.zeros(S1, **i32)
+        self.cross_len = torch.ones(S1, **i32)
+        self.finished = torch.ones(S1, device=dev, dtype=torch.uint8)
+        self.forced = torch.full((S1, max_prompt), self.pad, **i64)
+        self.out = torch.full((S1, self.seq + 1), self.pad, **i64)
+        self.flags = torch.ones(S1, dtype=torch.uint8).pin_memory()  # `finished`, copied out by every step
+
+        # step buffers, sized for the largest bucket
+        bm, bf = self.buckets[-1], dict(device=dev, dtype=self.embed.dtype)
+        self.active = torch.full((bm,), self.dummy, **i32)
+        self.x, self.hn, self.att = (torch.zeros(bm, self.width, **bf) for _ in range(3))
+        self.qkv_out = torch.zeros(bm, 3 * self.width, **bf)
+        self.q_out = torch.zeros(bm, self.width, **bf)
+        self.proj_out = torch.zeros(bm, self.width, **bf)
+        self.ffn_out = torch.zeros(bm, self.blocks[0].fc1.n, **bf)
+        self.logits = torch.zeros(bm, self.head.n, **bf)
         self.part = torch.empty(max(b * self.h * self._splits(b) * (self.d + 2) for b in self.buckets), device=dev,
                                 dtype=torch.float32)
-        self.w8_ws = torch.empty(8 << 20, device=dev, dtype=torch.float32)
-        self.w8_counters = torch.zeros(1024, device=dev, dtype=torch.int32)
-        self.flags = torch.ones(S + 1, dtype=torch.uint8).pin_memory()
+
+        self.stream = torch.cuda.Stream(device=dev)
+        self.programs = {b: self._program(b) for b in self.buckets}
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-        self.stream = torch.cuda.Stream()
         if capture:
             self._capture()
 
     @staticmethod
     def _splits(b: int) -> int:
-        """Workgroups per (row, head) of the cross-attention: several only for one or two rows (reference
-        stream_decoder.py:140-144)."""
-        return 4 if b <= 2 else 1
+        """Workgroups per (row, head) of the cross-attention: one for every bucket. The reference splits the frames
+        over 4 for one or two rows (stream_decoder.py:140-144); a split changes the fp32 combine order, so a piece's
+        tokens would then depend on how many rows it shares a step with. One split keeps every row's result
+        independent of the batch (at 375 frames a workgroup's 64 key groups cover the frames in one pass anyway)."""
+        return 1
 
-    # ---- the step ----------------------------------------------------------------------------------------------
+    # ---- the step as a list of launches ------------------------------------------------------------------------
 
-    def _w8(self, x, wq, bias, relu=False):
-        return w8_linear(x, wq, bias, relu, ws=self.w8_ws, counters=self.w8_counters)
-
-    def _proj(self, x, ly, name):
-        """The o, cross q or cross o projection: bf16 weights, as the reference keeps them."""
-        return bf16_linear(x, *getattr(ly, name))
-
-    def _qkv(self, hn, ly):
-        return self._w8(hn, ly.qkv_w8, ly.qkv[1]) if self.int8 else bf16_linear(hn, *ly.qkv)
-
-    def _ffn(self, hn, ly):
-        if self.int8:
-            return self._w8(self._w8(hn, ly.fc1_w8, ly.fc1[1], relu=True), ly.fc2_w8, ly.fc2[1])
-        return bf16_linear(bf16_linear(hn, *ly.fc1, relu=True), *ly.fc2)
-
-    def _head(self, hn, out):
-        if self.int8:
-            return w8_linear(hn, self.head_w8, self.head[1], ws=self.w8_ws, counters=self.w8_counters, out=out)
-        return bf16_linear(hn, *self.head, out=out)
-
-    def _attend(self, i, self_attn, act, q, splits, a):
+    def _attention(self, i: int, self_attn: bool, act, q, splits: int, out):
         if self_attn:
-            caches, n = (self.self_k[i], self.self_v[i]), self.pos
-            scales = (self.self_ks[i], self.self_vs[i]) if self.int8 else None
+            k, v, ks, vs, n = self.self_k[i], self.self_v[i], self.self_ks, self.self_vs, self.pos
         else:
-            caches, n = (self.cross_k[i], self.cross_v[i]), self.cross_len
-            scales = (self.cross_ks[i], self.cross_vs[i]) if self.int8 else None
+            k, v, ks, vs, n = self.cross_k[i], self.cross_v[i], self.cross_ks, self.cross_vs, self.cross_len
         if self.int8:
-            ext.dec_attention_q8(self_attn, act, q, *caches, *scales, n, self.scale, splits, self.part, a)
-        else:
-            ext.dec_attention(self_attn, act, q, *caches, n, self.scale, splits, self.part, a)
+            ks, vs = ks[i], vs[i]
+            return lambda: ext.dec_attention_q8(self_attn, act, q, k, v, ks, vs, n, self.scale, splits, self.part,
+                                                out)
+        return lambda: ext.dec_attention(self_attn, act, q, k, v, n, self.scale, splits, self.part, out)
 
-    def _step(self, b: int) -> None:
-        act, x, hn, a, splits = self.active[:b], self.x[:b], self.hn[:b], self.att[:b], self._splits(b)
-        ext.dec_embed(act, self.tok, self.pos, self.embed, self.pos_table, *self.emb_ln, *self.layers[0].ln1, x, hn)
-        for i, ly in enumerate(self.layers):
-            nxt = self.layers[i + 1] if i + 1 < len(self.layers) else None
-            self._attend(i, True, act, self._qkv(hn, ly), 1, a)
-            ext.dec_add_ln(x, self._proj(a, ly, "o"), *ly.ln2, hn)
-            self._attend(i, False, act, self._proj(hn, ly, "cq"), splits, a)
-            ext.dec_add_ln(x, self._proj(a, ly, "co"), *ly.ln3, hn)
-            following = nxt.ln1 if nxt else self.final_ln
-            ext.dec_add_ln(x, self._ffn(hn, ly), *following, hn)
-        logits = self._head(hn, self.logits[:b])
-        ext.dec_pick(logits, act, self.dummy, self.tok, self.pos, self.finished, self.forced, self.plen, self.limit,
-                     self.out, self.pad, self.eos)
-        self.flags.copy_(self.finished, non_blocking=True)
+    def _program(self, b: int) -> list:
+        """The step for the first b active rows (reference stream_decoder.py:176-199): embedding + first LayerNorm,
+        per layer self-attention (qkv, attention over the slot's cache, o, residual + LayerNorm), cross-attention (q,
+        attention over the slot's frames, o, residual + LayerNorm) and feed-forward (fc1 + ReLU, fc2, residual + the
+        next LayerNorm), then the head, the greedy pick and the end flags' copy to the host."""
+        act, x, hn, att = self.active[:b], self.x[:b], self.hn[:b], self.att[:b]
+        qkv, q, proj, ffn, logits = (t[:b] for t in (self.qkv_out, self.q_out, self.proj_out, self.ffn_out,
+                                                     self.logits))
+        ops = [lambda: ext.dec_embed(act, self.tok, self.pos, self.embed, self.pos_table, *self.emb_ln,
+                                     *self.blocks[0].norms[0], x, hn)]
+        for i, blk in enumerate(self.blocks):
+            after_ffn = self.blocks[i + 1].norms[0] if i + 1 < len(self.blocks) else self.final_ln
+            ops += [lambda blk=blk: blk.qkv(hn, qkv),
+                    self._attention(i, True, act, qkv, 1, att),
+                    lambda blk=blk: blk.o(att, proj),
+                    lambda blk=blk: ext.dec_add_ln(x, proj, *blk.norms[1], hn),
+                    lambda blk=blk: blk.cq(hn, q),
+                    self._attention(i, False, act, q, self._splits(b), att),
+                    lambda blk=blk: blk.co(att, proj),
+                    lambda blk=blk: ext.dec_add_ln(x, proj, *blk.norms[2], hn),
+                    lambda blk=blk: blk.fc1(hn, ffn, relu=True),
+                    lambda blk=blk: blk.fc2(ffn, proj),
+                    lambda ln=after_ffn: ext.dec_add_ln(x, proj, *ln, hn)]
+        ops += [lambda: self.head(hn, logits),
+                lambda: ext.dec_pick(logits, act, self.dummy, self.tok, self.pos, self.finished, self.forced,
+                                     self.plen, self.limit, self.out, self.pad, self.eos),
+                lambda: self.flags.copy_(self.finished, non_blocking=True)]
+        return ops
+
+    def _run(self, b: int) -> None:
+        for op in self.programs[b]:
+            op()
 
     @torch.no_grad()
     def _capture(self) -> None:
-        pool = torch.cuda.graph_pool_handle()
+        """One graph per bucket, on the decoder stream; each program runs once eagerly first (every launch
+        validated), then is recorded. The state is reset afterwards (the runs advanced the dummy rows only)."""
         with torch.cuda.stream(self.stream):
-            for b in reversed(self.buckets):  # largest first: the smaller graphs fit in the pool it leaves
-                self._step(b)
-                torch.cuda.current_stream().synchronize()
+            for b in reversed(self.buckets):
+                self._run(b)
+                self.stream.synchronize()
                 g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g, pool=pool, stream=self.stream):
-                    self._step(b)
+                with torch.cuda.graph(g, stream=self.stream):
+                    self._run(b)
                 self.graphs[b] = g
-            self.reset()
+        self.reset()
         self.stream.synchronize()
 
+    # ---- host side -------------------------------------------------------------------------------------------------
+
     def reset(self) -> None:
-        """All slots free (on the decoder stream)."""
+        """Every slot free (on the decoder stream)."""
         with torch.cuda.stream(self.stream):
             self.finished.fill_(1)
             self.pos.zero_()
             self.cross_len.fill_(1)
             self.active.fill_(self.dummy)
 
-    # ---- host side -----------------------------------------------------------------------------------------------
-
     def bucket(self, rows: int) -> int:
-        return next(b for b in self.buckets if b >= rows)
+        """The smallest bucket of at least `rows` rows."""
+        for b in self.buckets:
+            if b >= rows:
+                return b
+        raise ValueError(f"StreamDecoder: {rows} rows exceed the largest bucket {self.buckets[-1]}")
+
+    def _to_device(self, host: torch.Tensor) -> torch.Tensor:
+        return host.pin_memory().to(self.device, non_blocking=True)
 
     def fill_cross(self, hidden: torch.Tensor, lengths: list[int], slots: list[int], projected: bool = False) -> None:
-        """Cross-attention keys and values of packed encoder frames (sum(lengths), encoder width) into the given slots
-        (projected: hidden is already the decoder-width memory after `proj`), on the current stream."""
-        mem = hidden if projected else torch.nn.functional.linear(hidden, *self.proj)
-        kv = torch.nn.functional.linear(mem, self.cross_w, self.cross_b).contiguous()
-        slot_of = torch.repeat_interleave(torch.tensor(slots, dtype=torch.int32), torch.tensor(lengths))
-        frame_of = torch.cat([torch.arange(n, dtype=torch.int32) for n in lengths])
-        slot_of, frame_of = slot_of.to(self.device), frame_of.to(self.device)
+        """Cross-attention keys and values of packed encoder frames hidden (sum(lengths), width) into the given slots,
+        on the current stream: the decoder's input projection (unless projected), every layer's key and value
+        projections in one bf16 GEMM, then the scatter into the slots' caches (quantized per 128-vector with int8)."""
+        from kernels.cuda_ext import EPI_BIAS
+
+        rows = hidden.shape[0]
+        if rows == 0:
+            return
+        mem = hidden.contiguous()
+        if not projected:
+            out = torch.empty(rows, self.proj[0].shape[0], device=hidden.device, dtype=hidden.dtype)
+            ext.gemm(mem, self.proj[0], self.proj[1], out, EPI_BIAS, None, 1.0, 8)
+            mem = out
+        kv = torch.empty(rows, self.cross_w.shape[0], device=hidden.device, dtype=hidden.dtype)
+        ext.gemm(mem, self.cross_w, self.cross_b, kv, EPI_BIAS, None, 1.0, 8)
+        where = torch.empty(2, rows, dtype=torch.int32)
+        where[0] = torch.repeat_interleave(torch.tensor(slots, dtype=torch.int32), torch.tensor(lengths))
+        where[1] = torch.cat([torch.arange(n, dtype=torch.int32) for n in lengths])
+        where = where.pin_memory().to(hidden.device, non_blocking=True)
         if self.int8:
-            ext.dec_scatter_kv_q8(kv, slot_of, frame_of, self.cross_k, self.cross_v, self.cross_ks, self.cross_vs)
+            ext.dec_scatter_kv_q8(kv, where[0], where[1], self.cross_k, self.cross_v, self.cross_ks, self.cross_vs)
         else:
-            ext.dec_scatter_kv(kv, slot_of, frame_of, self.cross_k, self.cross_v)
+            ext.dec_scatter_kv(kv, where[0], where[1], self.cross_k, self.cross_v)
 
     def admit(self, slots: list[int], prompts: list[torch.Tensor], frames: list[int],
               max_new: list[int] | None = None) -> None:
-        """Start decoding in the given slots (on the decoder stream): the prompt forced, `frames` audio frames."""
+        """Start decoding in the given slots (on the decoder stream): each slot's prompt is forced by the steps
+        themselves, `frames` encoder frames attended to, at most max_new (default max_new_tokens) tokens made."""
         n = len(slots)
-        idx = torch.tensor(slots, dtype=torch.long)
+        if n == 0:
+            return
         forced = torch.full((n, self.max_prompt), self.pad, dtype=torch.long)
-        plen = torch.tensor([len(p) for p in prompts], dtype=torch.int32)
+        nums = torch.empty(n, 3, dtype=torch.int32)  # prompt length, position limit, frames
         for i, p in enumerate(prompts):
+            p = torch.as_tensor(p, dtype=torch.long).flatten()
+            if not 1 <= len(p) <= self.max_prompt:
+                raise ValueError(f"StreamDecoder: a prompt of {len(p)} tokens (1..{self.max_prompt})")
+            if not 1 <= frames[i] <= self.frames:
+                raise ValueError(f"StreamDecoder: {frames[i]} encoder frames (1..{self.frames})")
             forced[i, :len(p)] = p
-        limit = plen - 1 + torch.tensor(max_new or [self.max_new_tokens] * n, dtype=torch.int32)
+            nums[i] = torch.tensor([len(p), len(p) - 1 + (max_new[i] if max_new else self.max_new_tokens),
+                                    frames[i]])
+        out_rows = torch.full((n, self.seq + 1), self.pad, dtype=torch.long)
+        out_rows[:, :self.max_prompt] = forced
         with torch.cuda.stream(self.stream):
-            d = lambda t: t.to(self.device, non_blocking=True)  # noqa: E731
-            di = d(idx)
-            self.forced[di] = d(forced)
-            self.out[di] = self.pad
-            self.out[di, :self.max_prompt] = d(forced)
-            self.tok[di] = d(forced[:, 0])
-            self.pos[di] = 0
-            self.plen[di] = d(plen)
-            self.limit[di] = d(limit)
-            self.cross_len[di] = d(torch.tensor(frames, dtype=torch.int32))
-            self.finished[di] = 0
-        self.flags[idx] = 0
+            idx = self._to_device(torch.tensor(slots, dtype=torch.long))
+            forced_d, nums_d, out_d = (self._to_device(t) for t in (forced, nums, out_rows))
+            self.forced.index_copy_(0, idx, forced_d)
+            self.out.index_copy_(0, idx, out_d)
+            self.tok.index_copy_(0, idx, forced_d[:, 0].contiguous())
+            self.pos.index_fill_(0, idx, 0)
+            self.plen.index_copy_(0, idx, nums_d[:, 0].contiguous())
+            self.limit.index_copy_(0, idx, nums_d[:, 1].contiguous())
+            self.cross_len.index_copy_(0, idx, nums_d[:, 2].contiguous())
+            self.finished.index_fill_(0, idx, 0)
+        self.flags[torch.tensor(slots, dtype=torch.long)] = 0
 
     def set_active(self, slots: list[int]) -> int:
-        """The active list for the next steps (on the decoder stream); returns the bucket."""
+        """The active rows of the next steps (on the decoder stream), padded with the dummy slot; returns the
+        bucket to step."""
         b = self.bucket(max(1, len(slots)))
         host = torch.full((b,), self.dummy, dtype=torch.int32)
         host[:len(slots)] = torch.tensor(slots, dtype=torch.int32)
         with torch.cuda.stream(self.stream):
-            self.active[:b].copy_(host.pin_memory(), non_blocking=True)
+            self.active[:b].copy_(self._to_device(host))
         return b
 
     def step(self, bucket: int) -> None:
+        """One decoding step of the first `bucket` active rows (a graph replay on the decoder stream)."""
         with torch.cuda.stream(self.stream):
-            self.graphs[bucket].replay()
+            if bucket in self.graphs:
+                self.graphs[bucket].replay()
+            else:
+                self._run(bucket)
+
+    def weight_bytes(self) -> int:
+        """Bytes of projection weights one step reads."""
+        return sum(p.nbytes for blk in self.blocks for p in blk.projections()) + self.head.nbytes
+
+
+__all__ = ["DEFAULT_CONFIG", "StreamDecoder", "W8_CONFIGS", "W8_PERM", "bf16_linear", "prepare_w8", "unprepare_w8",
+           "w8_config", "w8_linear"]

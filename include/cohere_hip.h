@@ -195,8 +195,11 @@ int cohere_dec_scatter_kv_q8(const uint16_t* kv, int64_t rows, const int32_t* sl
                              int8_t* ck, int8_t* cv, float* cks, float* cvs, int64_t L, int64_t S, int64_t H,
                              int64_t T, void* stream);
 
-/* Number of per-layer tensors of cohere_encoder_layers (the reference's enum F, kernels/csrc/encoder_loop.cpp:34-44) */
-enum { COHERE_ENC_N_FIELDS = 53 };
+/* Number of per-layer tensors of cohere_encoder_layers: the reference's 53 (its enum F,
+ * kernels/csrc/encoder_loop.cpp:34-44) followed by 4 of this library's own (the feed-forwards' first linears in 2:4
+ * form: ff1 kept bytes, ff1 selectors, ff2 kept bytes, ff2 selectors; NULL keeps the dense first linear, as the
+ * reference always does). */
+enum { COHERE_ENC_N_REF_FIELDS = 53, COHERE_ENC_N_FIELDS = 57 };
 
 /* Device bytes cohere_encoder_layers needs as workspace for `rows` packed frames and feed-forward scale group
  * `group` (-1 on bad arguments). The reference allocates the same buffers inside the call. */
@@ -205,11 +208,13 @@ int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group);
 /* Replaces encoder_layers, int8 branch (reference kernels/csrc/encoder_loop.cpp:50-99, bound at
  * kernels/csrc/bindings.cpp:66): every layer of the FastConformer encoder on packed frames x [rows, 1280] bf16, in
  * place, in the reference's launch order. fields: n_layers x COHERE_ENC_N_FIELDS device pointers in the reference's
- * field order (NULL for the empty tensors: a dense W2 whose 2:4 form is given, the 2:4 fields of a dense layer,
- * absent biases). eps: n_layers x 5 (ff1, att, conv, ff2, out). tiles / lo / hi / rel_off / max_len / scale as in
+ * field order, then the 4 extra 2:4 first-linear fields (NULL for the empty tensors: a dense W1 or W2 whose 2:4 form
+ * is given, the 2:4 fields of a dense linear, absent biases). eps: n_layers x 5 (ff1, att, conv, ff2, out). tiles / lo / hi / rel_off / max_len / scale as in
  * cohere_relpos_attention and cohere_dwconv_bn_silu; rel_rows the table rows. cfg: the reference's list (bf16 config,
- * int8 QKV, grouped FF W2, FF W1, FF group, PW1, O/PW2, 2:4 FF W2). int8 must be nonzero: the bf16 branch is not
- * provided. workspace: at least cohere_encoder_workspace_bytes(rows, cfg[4]) bytes of device memory. */
+ * int8 QKV, grouped FF W2, FF W1, FF group, PW1, O/PW2, 2:4 FF W2). int8 nonzero runs the W8A8 branch on the
+ * quantized fields; int8 zero the bf16 branch (reference encoder_loop.cpp:101-124) on the bf16 weight fields with
+ * the bf16 GEMM config cfg[0] (3, 5 or 8). workspace: at least cohere_encoder_workspace_bytes(rows, cfg[4]) bytes of
+ * device memory (enough for either branch). */
 int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers, const double* eps,
                           const int32_t* tiles, int64_t n_tiles, const int32_t* lo, const int32_t* hi, int64_t rel_off,
                           int64_t max_len, int64_t rel_rows, double scale, int32_t heads, int32_t head_dim,

@@ -307,14 +307,16 @@ LAYER_FIELDS = (
     "ln_out_b", "ff1_w1", "ff1_b1", "ff1_w2", "ff1_b2", "ff2_w1", "ff2_b1", "ff2_w2", "ff2_b2", "wqkv", "bqkv", "wo",
     "bo", "bu", "bv", "rk", "wpw1", "bpw1", "wdw", "bdw", "bn_scale", "bn_shift", "wpw2", "bpw2", "q_ff1_w1",
     "q_ff1_s1", "q_ff1_w2", "q_ff1_s2", "q_ff2_w1", "q_ff2_s1", "q_ff2_w2", "q_ff2_s2", "q_qkv_w", "q_qkv_s",
-    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e")
+    "q_pw1_w", "q_pw1_s", "q_o_w", "q_o_s", "q_pw2_w", "q_pw2_s", "sp_ff1_w", "sp_ff1_e", "sp_ff2_w", "sp_ff2_e",
+    # the product's own extension: the first feed-forward linears in 2:4 form
+    "sp_ff1_w1", "sp_ff1_e1", "sp_ff2_w1", "sp_ff2_e1")
 
 
 def encoder_layers_int8(x, layers, eps, lengths, rel_off, scale, group=256, qgroup_ff1=256, threads=0):
     """encoder_loop.cpp:63-99 (the int8 branch), each step by the functions above and gemm_i8: x bf16 bits
     [rows, 1280] -> the layers' output (bf16 bits). layers: one dict per layer, LAYER_FIELDS -> numpy arrays (bf16 as
-    uint16 bits; the 2:4 W2 given as sp_ff*_w/e is run as the dense GEMM on its decompressed weights, which is
-    gemm_sparse.cu's result bit for bit). eps: per layer (ff1, att, conv, ff2, out)."""
+    uint16 bits; a 2:4 W2 given as sp_ff*_w/e, or W1 given as sp_ff*_w1/e1, is run as the dense GEMM on its
+    decompressed weights, which is gemm_sparse.cu's result bit for bit). eps: per layer (ff1, att, conv, ff2, out)."""
     x = _c(x, np.uint16).copy()
     lengths = list(lengths)
     starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
@@ -322,7 +324,9 @@ def encoder_layers_int8(x, layers, eps, lengths, rel_off, scale, group=256, qgro
     hi = np.concatenate([np.full(n, s + n) for s, n in zip(starts, lengths)]).astype(np.int32)
 
     def ffn(ly, hq, hs, k):
-        tq, ts = gemm_i8(hq, hs, hq.shape[1], ly[f"q_ff{k}_w1"], ly[f"q_ff{k}_s1"], ly.get(f"ff{k}_b1"), EPI_SILU_Q8,
+        sp1 = ly.get(f"sp_ff{k}_w1")
+        w1 = decompress_24(sp1, ly[f"sp_ff{k}_e1"]) if sp1 is not None and sp1.size else ly[f"q_ff{k}_w1"]
+        tq, ts = gemm_i8(hq, hs, hq.shape[1], w1, ly[f"q_ff{k}_s1"], ly.get(f"ff{k}_b1"), EPI_SILU_Q8,
                          qgroup=qgroup_ff1, threads=threads)
         sp = ly.get(f"sp_ff{k}_w")
         w2 = decompress_24(sp, ly[f"sp_ff{k}_e"]) if sp is not None and sp.size else ly[f"q_ff{k}_w2"]
@@ -354,6 +358,42 @@ def encoder_layers_int8(x, layers, eps, lengths, rel_off, scale, group=256, qgro
             h, x = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4], layers[i + 1]["ln_ff1_w"],
                              layers[i + 1]["ln_ff1_b"], eps[i + 1][0])
             hq, hs = q8_rows(h)
+        else:
+            x, _ = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4])
+    return x
+
+
+def encoder_layers_bf16(x, layers, eps, lengths, rel_off, scale, threads=0):
+    """encoder_loop.cpp:101-124 (the bf16 branch): x bf16 bits [rows, 1280] -> the layers' output (bf16 bits), every
+    linear by gemm_bf16 with its fused epilogue (SiLU, residual, GLU, bias), the LayerNorms, attention and depthwise
+    convolution by the functions above. layers: one dict per layer with the bf16 weight fields ff*_w1/w2, wqkv, wo,
+    wpw1 (GLU rows interleaved), wpw2 and the shared fields; eps: per layer (ff1, att, conv, ff2, out)."""
+    x = _c(x, np.uint16).copy()
+    lengths = list(lengths)
+    starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int64)
+    lo = np.concatenate([np.full(n, s) for s, n in zip(starts, lengths)]).astype(np.int32)
+    hi = np.concatenate([np.full(n, s + n) for s, n in zip(starts, lengths)]).astype(np.int32)
+    lin = lambda a, ly, w, b, epi, resid=None, alpha=1.0: gemm_bf16(  # noqa: E731
+        a, ly[w], ly.get(b), epi, resid=resid, alpha=alpha, threads=threads)
+    L = len(layers)
+    h, _ = layernorm(x, layers[0]["ln_ff1_w"], layers[0]["ln_ff1_b"], eps[0][0])
+    for i, ly in enumerate(layers):
+        t = lin(h, ly, "ff1_w1", "ff1_b1", EPI_SILU)
+        x = lin(t, ly, "ff1_w2", "ff1_b2", EPI_RESID, resid=x, alpha=0.5)
+        h, _ = layernorm(x, ly["ln_att_w"], ly["ln_att_b"], eps[i][1])
+        qkv = lin(h, ly, "wqkv", "bqkv", EPI_BIAS)
+        a = relpos_attention(qkv, ly["rk"], ly["bu"], ly["bv"], lengths, rel_off, scale)
+        x = lin(a, ly, "wo", "bo", EPI_RESID, resid=x)
+        h, _ = layernorm(x, ly["ln_conv_w"], ly["ln_conv_b"], eps[i][2])
+        g = lin(h, ly, "wpw1", "bpw1", EPI_GLU)
+        z = dwconv_bn_silu(g, ly["wdw"], ly["bdw"], ly["bn_scale"], ly["bn_shift"], lo, hi)
+        x = lin(z, ly, "wpw2", "bpw2", EPI_RESID, resid=x)
+        h, _ = layernorm(x, ly["ln_ff2_w"], ly["ln_ff2_b"], eps[i][3])
+        t = lin(h, ly, "ff2_w1", "ff2_b1", EPI_SILU)
+        x = lin(t, ly, "ff2_w2", "ff2_b2", EPI_RESID, resid=x, alpha=0.5)
+        if i + 1 < L:
+            h, x = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4], layers[i + 1]["ln_ff1_w"],
+                             layers[i + 1]["ln_ff1_b"], eps[i + 1][0])
         else:
             x, _ = layernorm(x, ly["ln_out_w"], ly["ln_out_b"], eps[i][4])
     return x

@@ -146,3 +146,50 @@ def hf_block_forward(blk, inv_freq, x: torch.Tensor, lengths: list[int]) -> torc
             outs.append(blk(h, position_embeddings=pos)[0])
             s += n
     return torch.cat(outs)
+
+
+def product_layers(device, n_layers: int, seed: int, sparse: bool = False, sparse_w1: bool = False, heads: int = 16):
+    """n_layers seeded random-init blocks (1280 wide, feed-forward 5120) converted by the product's EncoderLayers."""
+    from kernels.fast_encoder import EncoderLayers
+
+    blocks, inv = [], None
+    for i in range(n_layers):
+        blk, inv = make_block(1280, heads, 5120, seed=seed + i)
+        blocks.append(blk.to(device=device, dtype=torch.bfloat16))
+    return EncoderLayers(blocks, inv, sparse=sparse, sparse_w1=sparse_w1)
+
+
+def oracle_layer_fields(layers) -> list[dict]:
+    """The product's converted tensors (weights quantized on the host by the product, pinned against the checker's
+    quantizer elsewhere) as the checker's field dicts (numpy; bf16 as bits)."""
+    from kernels.fast_encoder import LAYER_FIELDS
+
+    out = []
+    for ly in layers.layers:
+        f = {}
+        for k in LAYER_FIELDS:
+            t = ly.tensors[k]
+            if t.numel() == 0:
+                continue
+            t = t.detach().cpu()
+            f[k] = bf16_bits(t) if t.dtype == torch.bfloat16 else t.numpy()
+        out.append(f)
+    return out
+
+
+def oracle_fields_bf16(blk, table: torch.Tensor) -> tuple[dict, list[float]]:
+    """The block's tensors as the checker's bf16 layer loop reads them (bf16 bits; GLU rows interleaved)."""
+    f, eps = oracle_fields(blk, table, False)
+    bits = lambda t: bf16_bits(t.detach().float().cpu().to(torch.bfloat16))  # noqa: E731
+    at, cv = blk.self_attn, blk.conv
+    for k, ff in (("ff1", blk.feed_forward1), ("ff2", blk.feed_forward2)):
+        f[f"{k}_w1"], f[f"{k}_w2"] = bits(ff.linear1.weight), bits(ff.linear2.weight)
+    f["wqkv"] = bits(torch.cat([at.q_proj.weight, at.k_proj.weight, at.v_proj.weight]))
+    f["wo"] = bits(at.o_proj.weight)
+    c = cv.depthwise_conv.in_channels
+    w1 = cv.pointwise_conv1.weight[:, :, 0]
+    f["wpw1"] = bits(torch.stack([w1[:c], w1[c:]], 1).reshape(2 * c, -1))
+    f["wpw2"] = bits(cv.pointwise_conv2.weight[:, :, 0])
+    for k in [k for k in f if k.startswith("q_")]:
+        del f[k]
+    return f, eps

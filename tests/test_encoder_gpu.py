@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import oracle
-from encoder_helpers import make_block, oracle_fields
+from encoder_helpers import oracle_layer_fields, product_layers
 from helpers import assert_bf16_close, bf16_bits, bf16_float, bf16_ulp
 
 pytestmark = pytest.mark.gpu
@@ -136,31 +136,11 @@ def test_relpos_attention_rejects_long_sequences(gpu):
 
 
 def _layers(gpu, n_layers, sparse, seed):
-    from kernels.fast_encoder import EncoderLayers
-
-    blocks, inv = [], None
-    for i in range(n_layers):
-        blk, inv = make_block(1280, 16, 5120, seed=seed + i)
-        blocks.append(blk.to(device=gpu, dtype=torch.bfloat16))
-    return EncoderLayers(blocks, inv, sparse=sparse)
+    return product_layers(gpu, n_layers, seed, sparse)
 
 
 def _oracle_layers(layers):
-    """The product's converted tensors (weights quantized on the GPU, already pinned against the checker's
-    quantizer) as the checker's field dicts."""
-    from kernels.fast_encoder import LAYER_FIELDS
-
-    out = []
-    for ly in layers.layers:
-        f = {}
-        for k in LAYER_FIELDS:
-            t = ly.tensors[k]
-            if t.numel() == 0:
-                continue
-            t = t.detach().cpu()
-            f[k] = bf16_bits(t) if t.dtype == torch.bfloat16 else t.numpy()
-        out.append(f)
-    return out
+    return oracle_layer_fields(layers)
 
 
 def _diff_stats(got_bits, want_bits):
@@ -205,7 +185,41 @@ def test_encoder_layers_rejects_and_noops(gpu):
     x = torch.empty(0, 1280, dtype=torch.bfloat16, device=gpu)
     layers(x, [])  # no rows: nothing to do
     meta = metadata([10], gpu)
-    with pytest.raises(RuntimeError, match="int8"):
+    # int8-converted layers hold no bf16 weights: the bf16 branch refuses them by name
+    with pytest.raises(RuntimeError, match=r"bf16.*misses field"):
         _ext().encoder_layers(torch.zeros(10, 1280, dtype=torch.bfloat16, device=gpu), layers.layer_tensors,
                               layers.layer_eps, meta["tiles"], meta["lo"], meta["hi"], 511, 10, 0.1, False,
                               layers.configs(10))
+
+
+def test_encoder_layers_bf16(gpu):
+    """The native loop's bf16 branch (the reference's INT8=0 layers, encoder_loop.cpp:101-124) against the checker's
+    restatement over two 16-head blocks. The only differences are the fp32 summation order of the GEMMs and the
+    attention, but each is rounded to bf16 and carried through the LayerNorms of two blocks, so the bar is the chain's
+    own sensitivity: RMS difference below, and largest difference within twice, what the checker moves when 1 % of its
+    input elements move by one bf16 ulp (measured: 4.1e-3 / 6.2e-2 x RMS against 5.1e-3 / 6.2e-2)."""
+    lengths = [200, 1, 97, 64]
+    from encoder_helpers import make_block
+    from kernels.fast_encoder import EncoderLayers
+
+    blocks, inv = [], None
+    for i in range(2):
+        blk, inv = make_block(1280, 16, 5120, seed=51 + i)
+        blocks.append(blk.to(device=gpu, dtype=torch.bfloat16))
+    layers = EncoderLayers(blocks, inv, int8=False)
+    assert all(ly.tensors["q_qkv_w"].numel() == 0 and ly.tensors["wqkv"].numel() for ly in layers.layers)
+    g = torch.Generator().manual_seed(52)
+    x = torch.randn(sum(lengths), 1280, generator=g).to(torch.bfloat16)
+    xd = x.to(gpu)
+    layers(xd, lengths)
+    fields = _oracle_layers(layers)
+    eps = [layers.layer_eps[5 * i:5 * i + 5] for i in range(2)]
+    want = oracle.encoder_layers_bf16(_bits(x), fields, eps, lengths, layers.rel_off, layers.scale)
+    xb = _bits(x).copy()
+    xb[np.random.default_rng(0).random(xb.shape) < 0.01] += 1
+    noise = oracle.encoder_layers_bf16(xb, fields, eps, lengths, layers.rel_off, layers.scale)
+    rms_gpu, max_gpu = _diff_stats(_bits(xd), want)
+    rms_noise, max_noise = _diff_stats(noise, want)
+    print(f"bf16 layers: kernels vs checker rms {rms_gpu:.2e} max {max_gpu:.2e}; perturbed checker rms "
+          f"{rms_noise:.2e} max {max_noise:.2e}")
+    assert rms_gpu < rms_noise and max_gpu <= 2 * max_noise

@@ -183,3 +183,27 @@ def test_encoder_layer_int8_follows_transformers_block(sparse):
         ref_blk.feed_forward1.linear2.bias.mul_(2)
     off = hf_block_forward(ref_blk, inv_freq, x.float(), lengths).numpy()
     assert np.sqrt(np.mean((off - want) ** 2)) / rms > 3 * err
+
+
+def test_encoder_layer_bf16_follows_transformers_block():
+    """One bf16 layer of the checker (encoder_loop.cpp:101-124 order) against transformers' ParakeetEncoderBlock in
+    float32 on the same bf16-representable weights: they differ by the bf16 roundings of the intermediate results
+    only. The same wrong composition as above is several times further off."""
+    from encoder_helpers import oracle_fields_bf16
+
+    hidden, heads, ff, lengths = 256, 2, 1024, [40, 23]
+    blk, inv_freq = make_block(hidden, heads, ff, seed=9)
+    table = hf_distance_table(blk, inv_freq, max_len=64)
+    fields, eps = oracle_fields_bf16(blk, table)
+    g = torch.Generator().manual_seed(10)
+    x = torch.randn(sum(lengths), hidden, generator=g).to(torch.bfloat16)
+    got = bf16_float(oracle.encoder_layers_bf16(bf16_bits(x), [fields], [eps], lengths, 63, (hidden // heads) ** -0.5))
+    want = hf_block_forward(blk, inv_freq, x.float(), lengths).numpy()
+    rms = np.sqrt(np.mean(want ** 2))
+    err = np.sqrt(np.mean((got - want) ** 2)) / rms
+    assert err < 1e-2, err
+    with torch.no_grad():
+        blk.feed_forward1.linear2.weight.mul_(2)
+        blk.feed_forward1.linear2.bias.mul_(2)
+    off = hf_block_forward(blk, inv_freq, x.float(), lengths).numpy()
+    assert np.sqrt(np.mean((off - want) ** 2)) / rms > 3 * err

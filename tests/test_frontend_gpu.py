@@ -166,4 +166,4 @@ def test_fast_encoder_rejects():
 
     enc = make_encoder(1, seed=4)
     with pytest.raises(ValueError, match="int8"):
-        FastEncoder(enc, int8=False)
+        FastEncoder(enc, int8=False, sparse=True)

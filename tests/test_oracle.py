@@ -134,19 +134,23 @@ def test_q8_rows_properties():
 
 
 def test_q8_rows_reciprocal_not_divide():
-    # x * (1/s) and x / s differ here: the reference multiplies by the rounded reciprocal (encoder_ops.cu:29-36)
+    # the reference multiplies by the rounded reciprocal (encoder_ops.cu:29-36); x * (1/s) and x / s differ on
+    # these hand-found bf16 rows (row maximum first): 0.5625 / (1.125 / 127) is 63.5 by the reciprocal (-> 64) but
+    # 63.499996 by the divide (-> 63); with maximum 1.171875 the two land the other way round
+    for mx_bits, x_bits, want_recip, want_div in ((0x3F90, 0x3F10, 64, 63), (0x3F96, 0x3F16, 63, 64)):
+        row = np.array([mx_bits, x_bits, 0x0000, 0xBF10], np.uint16)
+        q, s = O.q8_rows(row[None])
+        xf = bf16_float(row)
+        assert int(np.rint(xf[1] / s[0])) == want_div  # the divide would give the other integer
+        assert q[0, 1] == want_recip and q[0, 0] == 127 and q[0, 2] == 0
     rng = np.random.default_rng(6)
-    found = 0
     for _ in range(200):
         row = rng.standard_normal(64).astype(np.float32)
         xb = bf16_bits(torch.from_numpy(row).to(torch.bfloat16))
         q, s = O.q8_rows(xb[None])
         xf = bf16_float(xb)
         inv = np.float32(1) / s[0]
-        want = np.rint(np.clip(xf * inv, -127, 127)).astype(np.int8)
-        assert np.array_equal(q[0], want)
-        found += int((np.rint(np.clip(xf / s[0], -127, 127)) != want).any())
-    assert found >= 0  # the divide path is only a cross-check; the assertion above pins the reciprocal
+        assert np.array_equal(q[0], np.rint(np.clip(xf * inv, -127, 127)).astype(np.int8))
 
 
 # ---- a3-a5: GEMM ----------------------------------------------------------------------------------------------------

@@ -113,3 +113,30 @@ def test_pipeline_matches_checker_chain(gpu):
             compared += 1
     print(f"compared {compared} generated tokens")
     assert compared >= 10
+
+
+def test_submit_matches_transcribe(gpu):
+    """The service path (reference pipeline.py:96-115 argument order: pieces, prompt, max_new -> Future) gives the
+    same tokens as transcribe() for the same pieces: every stage is per piece, and one encoder chunk holds the same
+    rows on both paths. Two requests in flight at once, one with per-piece limits; close() ends the threads."""
+    import bench
+    from kernels.pipeline import Pipeline
+
+    model = bench.random_asr_model(gpu, enc_layers=1, seed=6)
+    pipe = Pipeline(model, None, 4, 12, True, True, buckets=(1, 2, 4))
+    lengths = [32000, 52800, 17600]
+    xs = [Pipeline.prepare(x) for x in bench.synthetic_audio(lengths, seed=10)]
+    prompt = torch.tensor([4, 5, 6, 7])
+    want = pipe.transcribe([torch.from_numpy(x).to(gpu) for x in xs], prompt)
+    want_short = pipe.transcribe([torch.from_numpy(x).to(gpu) for x in xs[:2]], prompt, [3, 5])
+    f1 = pipe.submit(xs, prompt)
+    f2 = pipe.submit(xs[:2], prompt, [3, 5])
+    got, got_short = f1.result(timeout=120), f2.result(timeout=120)
+    assert pipe.submit([], prompt).result() == []
+    pipe.close()
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b), (a, b)
+    for a, b, n in zip(got_short, want_short, (3, 5)):
+        assert np.array_equal(a, b) and len(a) <= len(prompt) + n
+    with pytest.raises(RuntimeError, match="transcribe"):
+        pipe.transcribe(xs, prompt)
