@@ -22,7 +22,7 @@ LIB = os.path.join(OUT_DIR, "libcohere_hip.so")
 OBJ_DIR = os.path.join(ROOT, "_build")
 
 SOURCES = ["capi.cpp", "gemm_q8.hip", "gemm_q8_dense.hip", "gemm_q8_sparse.hip", "dec_w8.hip", "quant.hip",
-           "encoder_ops.hip", "encoder_loop.cpp", "decoder_ops.hip", "gemm_bf16.hip", "frontend.hip"]
+           "encoder_ops.hip", "encoder_loop.cpp", "encoder_noalloc.hip", "decoder_ops.hip", "gemm_bf16.hip", "frontend.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-fno-fast-math", f"-I{INCLUDE}", f"-I{CSRC}",

@@ -102,6 +102,11 @@ extern "C" int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group) {
   return std::max(carve(nullptr, rows, group).bytes, carve_bf16(nullptr, rows).bytes);
 }
 
+extern "C" int64_t cohere_encoder_branch_workspace_bytes(int64_t rows, int64_t group, int32_t int8) {
+  if (rows < 0 || group <= 0 || DFF % group) return -1;
+  return int8 ? carve(nullptr, rows, group).bytes : carve_bf16(nullptr, rows).bytes;
+}
+
 namespace {
 
 // The bf16 branch (reference kernels/csrc/encoder_loop.cpp:101-124): every linear a bf16 GEMM with its epilogue
@@ -191,7 +196,7 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
   const int64_t c_sp = n_cfg > 7 ? cfg[7] : 0;
   COHERE_REQUIRE(group > 0 && DFF % group == 0, "encoder_layers: the feed-forward group must divide 5120");
   if (rows == 0 || n_layers == 0) return 0;
-  const int64_t need = cohere_encoder_workspace_bytes(rows, group);
+  const int64_t need = cohere_encoder_branch_workspace_bytes(rows, group, int8);
   COHERE_REQUIRE(workspace && workspace_bytes >= need,
                  "encoder_layers: workspace needs " + std::to_string(need) + " bytes");
   if (!int8) {

@@ -33,7 +33,8 @@ EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_l
            "cohere_relpos_attention", "cohere_encoder_workspace_bytes", "cohere_encoder_layers", "cohere_dec_embed",
            "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
            "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8", "cohere_gemm_bf16", "cohere_logmel_workspace_bytes",
-           "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw")
+           "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw", "cohere_encoder_branch_workspace_bytes",
+           "cohere_encoder_layers_noalloc")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -68,6 +69,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_sub_dw": [P, P, P, P, I64, P, P, P, I64, I64, P],
         "cohere_encoder_layers": [P, I64, P, I64, P, P, I64, P, P, I64, I64, I64, ctypes.c_double, I32, I32, I32, P,
                                   I64, P, I64, P],
+        "cohere_encoder_layers_noalloc": [P, I64, P, I64, P, P, I64, P, P, I64, I64, I64, ctypes.c_double, I32, I32,
+                                          I32, P, I64, P],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)
@@ -75,6 +78,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         fn.restype = ctypes.c_int
     lib.cohere_encoder_workspace_bytes.argtypes = [I64, I64]
     lib.cohere_encoder_workspace_bytes.restype = I64
+    lib.cohere_encoder_branch_workspace_bytes.argtypes = [I64, I64, I32]
+    lib.cohere_encoder_branch_workspace_bytes.restype = I64
     lib.cohere_logmel_workspace_bytes.argtypes = [I64]
     lib.cohere_logmel_workspace_bytes.restype = I64
     lib.cohere_last_error.restype = ctypes.c_char_p
@@ -309,12 +314,8 @@ class _Ext:
     def encoder_workspace_bytes(self, rows: int, group: int) -> int:
         return int(self._lib.cohere_encoder_workspace_bytes(int(rows), int(group)))
 
-    def encoder_layers(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
-        """Every layer on packed frames x (N, 1280) bf16, in place, launched from native code
-        (kernels/csrc/encoder_loop.cpp:50-99). layers: per layer the tensors in the reference's field order
-        (fast_encoder.py:121-130), 53 of them, optionally followed by 4 more (the feed-forwards' first linears in
-        2:4 form: ff1 kept, ff1 selectors, ff2 kept, ff2 selectors); empty tensors stand for absent ones. int8: the
-        W8A8 branch on the quantized fields, else the bf16 branch on the bf16 weights (encoder_loop.cpp:101-124)."""
+    def _encoder_args(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
+        """The checked C arguments of an encoder_layers call (None when there is nothing to do)."""
         _check(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 2 and x.shape[1] == 1280,
                "encoder_layers: x (N, 1280) contiguous bf16")
         n_ref, n_fields = 53, 57
@@ -328,19 +329,41 @@ class _Ext:
         cfg = [int(c) for c in cfg]
         _check(len(cfg) >= 5, "encoder_layers: cfg needs at least 5 entries")
         if rows == 0 or not layers:
-            return
+            return None
         H, D = layers[0][22].shape  # bias_u: (heads, head size)
         ptrs = (ctypes.c_void_p * (n_fields * len(layers)))(
             *[t.data_ptr() if t.numel() > 0 else None for ly in layers
               for t in (*ly, *([_EMPTY] * (n_fields - len(ly))))])
         eps_arr = (ctypes.c_double * len(eps))(*[float(e) for e in eps])
         cfg_arr = (ctypes.c_int64 * len(cfg))(*cfg)
-        nbytes = self.encoder_workspace_bytes(rows, cfg[4])
+        return (_ptr(x), rows, ptrs, len(layers), eps_arr, _ptr(tiles), tiles.shape[0], _ptr(lo), _ptr(hi),
+                int(rel_off), int(max_len), layers[0][24].shape[0], float(scale), H, D, int(bool(int8)), cfg_arr,
+                len(cfg)), cfg
+
+    def encoder_layers(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
+        """Every layer on packed frames x (N, 1280) bf16, in place, launched from native code
+        (kernels/csrc/encoder_loop.cpp:50-124). layers: per layer the tensors in the reference's field order
+        (fast_encoder.py:121-130), 53 of them, optionally followed by 4 more (the feed-forwards' first linears in
+        2:4 form: ff1 kept, ff1 selectors, ff2 kept, ff2 selectors); empty tensors stand for absent ones. int8: the
+        W8A8 branch on the quantized fields, else the bf16 branch on the bf16 weights (encoder_loop.cpp:101-124).
+        The workspace is allocated here, through torch's caching allocator."""
+        packed = self._encoder_args(x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg)
+        if packed is None:
+            return
+        args, cfg = packed
+        nbytes = int(self._lib.cohere_encoder_branch_workspace_bytes(x.shape[0], cfg[4], int(bool(int8))))
         _check(nbytes >= 0, "encoder_layers: bad feed-forward group")
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-        self._call("cohere_encoder_layers", _ptr(x), rows, ptrs, len(layers), eps_arr, _ptr(tiles), tiles.shape[0],
-                   _ptr(lo), _ptr(hi), int(rel_off), int(max_len), layers[0][24].shape[0], float(scale), H, D,
-                   int(bool(int8)), cfg_arr, len(cfg), _ptr(ws), nbytes, _stream())
+        self._call("cohere_encoder_layers", *args, _ptr(ws), nbytes, _stream())
+
+    def encoder_layers_noalloc(self, x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg):
+        """encoder_layers with the library's own per-GPU scratch array in place of a workspace: allocates nothing
+        (no counterpart in the reference; for callers that cannot allocate). At most ~3900 int8-layer rows; calls
+        that overlap on one GPU race."""
+        packed = self._encoder_args(x, layers, eps, tiles, lo, hi, rel_off, max_len, scale, int8, cfg)
+        if packed is None:
+            return
+        self._call("cohere_encoder_layers_noalloc", *packed[0], _stream())
 
     # ---- decoder projections (bindings.cpp:55-56) -----------------------------------------------------------
 

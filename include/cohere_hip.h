@@ -205,6 +205,10 @@ enum { COHERE_ENC_N_REF_FIELDS = 53, COHERE_ENC_N_FIELDS = 57 };
  * `group` (-1 on bad arguments). The reference allocates the same buffers inside the call. */
 int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group);
 
+/* Device bytes the int8 (int8 nonzero) or bf16 branch of cohere_encoder_layers alone needs (-1 on bad arguments);
+ * cohere_encoder_workspace_bytes is the larger of the two. */
+int64_t cohere_encoder_branch_workspace_bytes(int64_t rows, int64_t group, int32_t int8);
+
 /* Replaces encoder_layers, int8 branch (reference kernels/csrc/encoder_loop.cpp:50-99, bound at
  * kernels/csrc/bindings.cpp:66): every layer of the FastConformer encoder on packed frames x [rows, 1280] bf16, in
  * place, in the reference's launch order. fields: n_layers x COHERE_ENC_N_FIELDS device pointers in the reference's
@@ -213,13 +217,26 @@ int64_t cohere_encoder_workspace_bytes(int64_t rows, int64_t group);
  * cohere_relpos_attention and cohere_dwconv_bn_silu; rel_rows the table rows. cfg: the reference's list (bf16 config,
  * int8 QKV, grouped FF W2, FF W1, FF group, PW1, O/PW2, 2:4 FF W2). int8 nonzero runs the W8A8 branch on the
  * quantized fields; int8 zero the bf16 branch (reference encoder_loop.cpp:101-124) on the bf16 weight fields with
- * the bf16 GEMM config cfg[0] (3, 5 or 8). workspace: at least cohere_encoder_workspace_bytes(rows, cfg[4]) bytes of
- * device memory (enough for either branch). */
+ * the bf16 GEMM config cfg[0] (3, 5 or 8). workspace: at least cohere_encoder_branch_workspace_bytes(rows, cfg[4],
+ * int8) bytes of device memory (cohere_encoder_workspace_bytes is enough for either branch). */
 int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers, const double* eps,
                           const int32_t* tiles, int64_t n_tiles, const int32_t* lo, const int32_t* hi, int64_t rel_off,
                           int64_t max_len, int64_t rel_rows, double scale, int32_t heads, int32_t head_dim,
                           int32_t int8, const int64_t* cfg, int64_t n_cfg, void* workspace, int64_t workspace_bytes,
                           void* stream);
+
+/* No counterpart in the reference. cohere_encoder_layers for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same arguments without the
+ * workspace. The loop's buffers live in a file-scope device array of COHERE_ENC_NOALLOC_BYTES (64 MiB) per GPU, held
+ * until the process ends; a call whose branch needs more (cohere_encoder_branch_workspace_bytes: above ~3900 rows of
+ * the int8 layers or ~2600 of the bf16 ones) fails with an error and launches nothing. The call allocates nothing.
+ * All calls on one GPU share its array: calls that overlap on one GPU (two streams, two threads) race. */
+enum { COHERE_ENC_NOALLOC_BYTES = 64 << 20 };
+int cohere_encoder_layers_noalloc(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers,
+                                  const double* eps, const int32_t* tiles, int64_t n_tiles, const int32_t* lo,
+                                  const int32_t* hi, int64_t rel_off, int64_t max_len, int64_t rel_rows, double scale,
+                                  int32_t heads, int32_t head_dim, int32_t int8, const int64_t* cfg, int64_t n_cfg,
+                                  void* stream);
 
 /* Bytes of device workspace cohere_logmel_features needs for total_frames frames (fp32 log-mel values). */
 int64_t cohere_logmel_workspace_bytes(int64_t total_frames);
