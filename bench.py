@@ -1,6 +1,6 @@
 """Benchmark of the MI355X quantized-GEMM hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--only dominant|step]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--no-traffic] [--only PART]
 
 Workload (the metric's configuration): one step = the 2:4-sparse W8A8 linear at
 M=3000 (8 clips x 375 frames), N=5120, K=1280 with bias, followed by the down projection M=3000, N=1280, K=5120
@@ -11,10 +11,12 @@ ops (2*M*N*K per GEMM) per second over the whole step, in TOPS.
 Timing: steps are captured into a HIP graph (torch.cuda.CUDAGraph; the kernels are launched on the current stream
 through the C ABI) and replayed; W warm-up steps, then exactly K timed steps between synchronizations, timed with HIP
 events on the launching stream. The roofline figure is the dominant kernel's: its own graph of back-to-back launches,
-timed with HIP events, priced against MI355X's sparse int8 peak (10.1 POPS dense-equivalent, i.e. 5.0 POPS of
-executed MFMA work). The CPU baseline is the oracle's C restatement (OpenMP, all host threads) on a bounded sample of
-the same workload (dense on the pruned weights, as the CPU has no 2:4 path), next to the reference's CPU path
-(torch._int_mm) on the same sample.
+timed with HIP events, priced against MI355X's sparse int8 peak (10.1 POPS dense-equivalent); its HBM traffic per
+launch comes from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) run as child processes of this run, scaled by a
+plain device copy's counts (null with --no-traffic or without rocprofv3). The CPU baseline is the reference's own
+CPU path (torch._int_mm + the fp32 epilogue, all host threads) on a bounded sample of the same workload (dense on the
+pruned weights, as the CPU has no 2:4 path); the checker's C port beside it. The same CPU leg runs config 4's chain on
+the host for two clips (oracle/chain.py) and reports the GPU tokens' agreement with it.
 
 Extras (not the metric): config 0 (dense W8A8 5120x1280, bias) TOPS against the dense peak; config 3's decoder-
 step projections (M=64, 8 layers + head, all int8 weights) in GB/s against 8 TB/s, cold-cache (weight sets rotated so
@@ -31,6 +33,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "cohere-inference_amd"))
@@ -41,6 +45,11 @@ PEAK_HBM = 8.0e12
 M, D, F = 3000, 1280, 5120
 
 
+def log(msg: str) -> None:
+    """A progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -48,7 +57,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "block", "decstep", "e2e"], default=None,
+    ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes for the traffic")
+    ap.add_argument("--only", choices=["dominant", "step", "dense", "decoder", "copy", "traffic", "block", "decstep",
+                                       "e2e"], default=None,
                     help="run one part only (for rocprofv3 runs)")
     ap.add_argument("--tile", type=int, default=-1, help="force a gfx950 GEMM tile (tuning)")
     return ap.parse_args()
@@ -110,94 +121,193 @@ def time_graph(g, replays):
     return e0.elapsed_time(e1) / replays
 
 
-def committed_traffic(which: str):
-    path = os.path.join(ROOT, "profiles", "gemm_sp_config1_traffic.json")
-    try:
-        table = json.load(open(path))
-    except (OSError, ValueError):
+def measure_traffic(timeout_s: int = 150):
+    """HBM bytes per launch of config 1's two GEMMs, measured now: two rocprofv3 --pmc passes over this script's
+    `--only traffic` mode (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads
+    for a plain 1 GiB device copy in the same pass (read 1 GiB, write 1 GiB). Runs the profiler as a child process
+    before this process touches the GPU. Returns {"up"|"down": {"kernel", "bytes", "read", "write"}, "factors"} or
+    None (no rocprofv3, or a pass failed or ran over its time limit)."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
         return None
-    from kernels.cuda_ext import ext  # noqa: F401
-    key = table.get("up" if "up" in which else "down")
-    return None if key is None else key["bytes"]
+    out = tempfile.mkdtemp(prefix="bench_pmc_", dir="/tmp")
+    env = dict(os.environ, TMPDIR="/tmp")
+    per = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        name = counter.lower()
+        cmd = [prof, "--pmc", counter, "-d", out, "-o", name, "--output-format", "csv", "--",
+               sys.executable, os.path.abspath(__file__), "--only", "traffic"]
+        p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                             start_new_session=True)
+        try:
+            p.wait(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(p.pid, signal.SIGKILL)
+            p.wait()
+            return None
+        if p.returncode != 0:
+            return None
+        path = next((os.path.join(dp, f) for dp, _, fs in os.walk(out) for f in fs
+                     if f.startswith(name) and f.endswith("counter_collection.csv")), None)
+        if path is None:
+            return None
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] == counter:
+                rows.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        per[counter] = rows
+    copy_name = next((k for k in per["FETCH_SIZE"] if "copyBuffer" in k), None)
+    gemms = sorted((k for k in per["FETCH_SIZE"] if "gemm_q8_kernel<" in k),
+                   key=lambda k: len(per["FETCH_SIZE"][k]))
+    if copy_name is None or len(gemms) != 2 or copy_name not in per["WRITE_SIZE"]:
+        return None
+    # the copy: 1 GiB read and written per call, two calls (evicted source each time)
+    fr = 2.0 * (1 << 30) / (1024.0 * sum(per["FETCH_SIZE"][copy_name]))
+    fw = 2.0 * (1 << 30) / (1024.0 * sum(per["WRITE_SIZE"][copy_name]))
+    res = {"factors": {"read": round(fr, 4), "write": round(fw, 4)}}
+    # the traffic mode launches the up projection 3 times and the down projection 5 times
+    for label, kname in zip(("up", "down"), gemms):
+        rd = 1024.0 * fr * float(np.mean(per["FETCH_SIZE"][kname])) if kname in per["FETCH_SIZE"] else None
+        wr = 1024.0 * fw * float(np.mean(per["WRITE_SIZE"].get(kname, [0.0])))
+        res[label] = {"kernel": kname, "read": int(rd), "write": int(wr), "bytes": int(rd + wr)}
+    shutil.rmtree(out, ignore_errors=True)
+    return res
 
 
-def cpu_baseline(target_s=10.0):
-    """The oracle (C, OpenMP over all host threads) on full config-1 steps, dense on the pruned weights, repeated
-    until target_s; plus torch._int_mm (the reference's CPU int8 path) on one step."""
-    import numpy as np
+def _cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline(target_s=12.0):
+    """The reference's own CPU path on a bounded sample of the metric's workload (the config-1 step: the up and down
+    projections, dense on the 2:4-pruned int8 weights, bias epilogue): torch._int_mm (int8 x int8 -> int32, the CPU
+    int8 matmul of the reference's non-CUDA path) plus the same fp32 epilogue (acc * x-scale * w-scale + bias, rounded
+    to bf16), on all host threads; three rounds of about target_s / 3 seconds each, value = the best round's mean.
+    Side keys: the same at one thread, the checker's C port on the same step, and config 3's 49 decoder projections
+    through torch._int_mm."""
     import torch
 
     import oracle as O
 
     threads = os.cpu_count() or 1
-    rng = np.random.default_rng(0)
-    xq = rng.integers(-127, 128, (M, D)).astype(np.int8)
-    xs = np.full(M, 0.01, np.float32)
-    xdq = rng.integers(-127, 128, (M, F)).astype(np.int8)
-    w_up = rng.integers(-127, 128, (F, D)).astype(np.int8)
-    w_dn = rng.integers(-127, 128, (D, F)).astype(np.int8)
-    for w in (w_up, w_dn):  # 2:4 pattern: dense on pruned
-        w.reshape(w.shape[0], -1, 4)[..., 2:] = 0
-    s_up, s_dn = np.full(F, 1e-3, np.float32), np.full(D, 1e-3, np.float32)
-    b_up = np.zeros(F, np.uint16)
-    b_dn = np.zeros(D, np.uint16)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    xq = torch.randint(-127, 128, (M, D), generator=g, dtype=torch.int8)
+    xdq = torch.randint(-127, 128, (M, F), generator=g, dtype=torch.int8)
+    xs = torch.rand(M, 1, generator=g) * 0.02
+    w_up = torch.randint(-127, 128, (F, D), generator=g, dtype=torch.int8)
+    w_dn = torch.randint(-127, 128, (D, F), generator=g, dtype=torch.int8)
+    for w in (w_up, w_dn):  # the 2:4 pattern: the CPU has no sparse path, so dense on the pruned weights
+        w.view(w.shape[0], -1, 4)[..., 2:] = 0
+    s_up, s_dn = torch.rand(F) * 1e-3, torch.rand(D) * 1e-3
+    b_up, b_dn = torch.randn(F) * 0.01, torch.randn(D) * 0.01
+    wt_up, wt_dn = w_up.t().contiguous(), w_dn.t().contiguous()
     ops = 2.0 * M * F * D * 2
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        O.gemm_i8(xq, xs, D, w_up, s_up, b_up, O.EPI_BIAS, threads=threads)
-        O.gemm_i8(xdq, xs, F, w_dn, s_dn, b_dn, O.EPI_BIAS, threads=threads)
-        steps += 1
-        if time.perf_counter() - t0 >= target_s:
-            break
-    dt = (time.perf_counter() - t0) / steps
-    torch.set_num_threads(threads)
-    a1, a2 = torch.from_numpy(xq), torch.from_numpy(xdq)
-    b1, b2 = torch.from_numpy(w_up).t().contiguous(), torch.from_numpy(w_dn).t().contiguous()
-    best = 1e9
-    for _ in range(3):
-        t = time.perf_counter()
-        torch._int_mm(a1, b1)
-        torch._int_mm(a2, b2)
-        best = min(best, time.perf_counter() - t)
+
+    def step():
+        for a, wt, sw, b in ((xq, wt_up, s_up, b_up), (xdq, wt_dn, s_dn, b_dn)):
+            acc = torch._int_mm(a, wt)
+            (acc.float().mul_(xs).mul_(sw).add_(b)).to(torch.bfloat16)
+
+    def rounds(seconds_each):
+        best = 1e9
+        for _ in range(3):
+            n, t0 = 0, time.perf_counter()
+            while True:
+                step()
+                n += 1
+                if time.perf_counter() - t0 >= seconds_each:
+                    break
+            best = min(best, (time.perf_counter() - t0) / n)
+        return best, n
+
+    step()
+    dt, n_last = rounds(target_s / 3)
     torch.set_num_threads(1)
-    t = time.perf_counter()
-    torch._int_mm(a1, b1)
-    torch._int_mm(a2, b2)
-    one = time.perf_counter() - t
+    dt1, _ = rounds(0.5)
     torch.set_num_threads(threads)
+    # the checker's C port (OpenMP over all host threads), same step
+    xq_n, xdq_n, xs_n = xq.numpy(), xdq.numpy(), xs.numpy()[:, 0].copy()
+    bb_up, bb_dn = (O.f32_to_bf16(b.numpy()) for b in (b_up, b_dn))
+    t0, k = time.perf_counter(), 0
+    while k == 0 or time.perf_counter() - t0 < 3.0:
+        O.gemm_i8(xq_n, xs_n, D, w_up.numpy(), s_up.numpy(), bb_up, O.EPI_BIAS, threads=threads)
+        O.gemm_i8(xdq_n, xs_n, F, w_dn.numpy(), s_dn.numpy(), bb_dn, O.EPI_BIAS, threads=threads)
+        k += 1
+    dt_port = (time.perf_counter() - t0) / k
     # config 3's decoder projections (M=64, int8 weights as int32-accumulating matmuls): one step's 49 calls
-    g = torch.Generator().manual_seed(3)
     dec = [(3072, 1024)] + [(1024, 1024)] * 3 + [(4096, 1024), (1024, 4096)]
-    xs64 = {k: torch.randint(-127, 128, (64, k), generator=g, dtype=torch.int8) for k in (1024, 4096)}
-    ws64 = [torch.randint(-127, 128, (k, n), generator=g, dtype=torch.int8) for n, k in dec]
+    xs64 = {kk: torch.randint(-127, 128, (64, kk), generator=g, dtype=torch.int8) for kk in (1024, 4096)}
+    ws64 = [torch.randint(-127, 128, (kk, n), generator=g, dtype=torch.int8) for n, kk in dec]
     head = torch.randint(-127, 128, (1024, 16384), generator=g, dtype=torch.int8)
-    dec_best, dec_bytes = 1e9, 8 * sum(n * k for n, k in dec) + 16384 * 1024
+    dec_best, dec_bytes = 1e9, 8 * sum(n * kk for n, kk in dec) + 16384 * 1024
     for _ in range(3):
         t = time.perf_counter()
         for _layer in range(8):
-            for (n, k), w in zip(dec, ws64):
-                torch._int_mm(xs64[k], w)
+            for (n, kk), w in zip(dec, ws64):
+                torch._int_mm(xs64[kk], w)
         torch._int_mm(xs64[1024], head)
         dec_best = min(dec_best, time.perf_counter() - t)
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{steps} full config-1 steps (3000x5120x1280 + 3000x1280x5120, dense on 2:4-pruned int8 "
-                      f"weights, bias epilogue) in {dt * steps:.1f} s, oracle/cohere_oracle.c",
-            "cpu_model": model,
-            "reference_cpu_path_int_mm": {"value": round(ops / best / 1e12, 4), "unit": "TOPS", "threads": threads,
-                                          "what": "torch._int_mm on the same step, int32 result only, best of 3",
-                                          "value_1_thread": round(ops / one / 1e12, 4)},
+    return {"value": round(ops / dt / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "reference",
+            "sample": f"the reference's CPU int8 path (torch._int_mm + fp32 dequant/bias epilogue to bf16) on full "
+                      f"config-1 steps (3000x5120x1280 + 3000x1280x5120, dense on 2:4-pruned int8 weights), best of 3 "
+                      f"rounds of ~{target_s / 3:.0f} s ({n_last} steps in the last), {threads} threads",
+            "cpu_model": _cpu_model_name(),
+            "value_1_thread": round(ops / dt1 / 1e12, 4),
+            "oracle_port": {"value": round(ops / dt_port / 1e12, 4), "unit": "TOPS", "threads": threads,
+                            "what": "the checker's C restatement (oracle/cohere_oracle.c, OpenMP) on the same step"},
             "reference_cpu_path_decoder_gemms": {"ms_per_step": round(dec_best * 1e3, 2),
                                                  "GBps": round(dec_bytes / dec_best / 1e9, 1), "threads": threads,
                                                  "what": "torch._int_mm on config 3's 49 step projections at M=64 "
                                                          "(int8 weights, int32 result), best of 3"}}
+
+
+def cpu_chain(model, pieces, gpu_tokens, prompt, max_new=448):
+    """Config 4 through the checker's whole chain on the CPU (oracle/chain.py: the reference pipeline's stages on the
+    host) for a few clips: its audio-sec/sec, and the agreement of the GPU's tokens with it. The checker decodes with
+    the GPU's tokens as its history (teacher forcing), so at every generated position it says which token the
+    reference path picks given the same history: agreement = the fraction of the GPU's generated tokens it picks
+    too; the free-running common prefix is the run of agreements from the start."""
+
+    from oracle import chain
+
+    t0 = time.perf_counter()
+    W = chain.asr_weights(model, int8=True, sparse=True, sparse_w1=True)
+    t1 = time.perf_counter()
+    log(f"  weights converted in {t1 - t0:.0f} s; encoding {len(pieces)} clips")
+    hidden, lengths = chain.encode(W, pieces)
+    t2 = time.perf_counter()
+    log(f"  encoded in {t2 - t1:.0f} s; decoding")
+    _, picks = chain.decode(W, hidden, lengths, prompt, max_new, forced_tokens=gpu_tokens)
+    t3 = time.perf_counter()
+    P = len(prompt)
+    same = total = 0
+    prefixes = []
+    for toks, pk in zip(gpu_tokens, picks):
+        gen = list(toks[P:])
+        eq = [int(a == b) for a, b in zip(gen, pk)]
+        same, total = same + sum(eq), total + len(gen)
+        prefixes.append(next((i for i, e in enumerate(eq) if not e), len(eq)))
+    audio_s = sum(len(p) for p in pieces) / 16000
+    return {"clips": len(pieces), "generated_tokens": total, "token_agreement": round(same / max(total, 1), 4),
+            "free_running_common_prefix": prefixes,
+            "cpu_reference_chain": {"audio_sec_per_sec": round(audio_s / (t3 - t1), 3), "encode_s": round(t2 - t1, 1),
+                                    "decode_s": round(t3 - t2, 1), "weights_s": round(t1 - t0, 1),
+                                    "threads": os.cpu_count() or 1,
+                                    "what": "oracle/chain.py (C restatement, OpenMP): features, stem, 24 int8 "
+                                            "layers, cross fill, greedy decode teacher-forced on the GPU's tokens"}}
 
 
 def decoder_extra(dev, reps_sets=4):
@@ -285,14 +395,14 @@ def random_block(seed: int, heads: int = 16, dev=None):
 
 
 def block_extra(dev, replays=20):
-    """Config 2: one random-init FastConformer block (16 heads, 2:4-sparse feed-forward W2s, every linear W8A8) on
+    """Config 2: one random-init FastConformer block (16 heads, both feed-forward linears 2:4, every linear W8A8) on
     x (8 x 375 = 3000 packed frames, N(0,1)), through the native layer loop, in a HIP graph."""
     import torch
 
     from kernels.fast_encoder import EncoderLayers, metadata
 
     blk, inv_freq = random_block(1, dev=dev)
-    layers = EncoderLayers([blk], inv_freq, sparse=True)
+    layers = EncoderLayers([blk], inv_freq, sparse=True, sparse_w1=True)
     lengths = [375] * 8
     meta = metadata(lengths, dev)
     g = torch.Generator().manual_seed(2)
@@ -302,7 +412,7 @@ def block_extra(dev, replays=20):
         graph.replay()
     ms = time_graph(graph, replays)
     gemm_ops = 2.0 * M * D * (4 * F + 3 * D + D + 2 * D + D)  # FF1/FF2 W1+W2, QKV, O, PW1 (GLU), PW2
-    return {"what": "config 2: one FastConformer block (d 1280, 16 heads of 80, FFN 5120 with 2:4 W2, conv module), "
+    return {"what": "config 2: one FastConformer block (d 1280, 16 heads of 80, FFN 5120 with both linears 2:4, conv module), "
                     "all linears W8A8, 8 x 375 packed frames, native layer loop (15 launches) in a HIP graph",
             "ms_per_block": round(ms, 4), "gemm_ops": gemm_ops,
             "gemm_TOPS_over_block": round(gemm_ops / (ms * 1e-3) / 1e12, 1),
@@ -449,8 +559,8 @@ def random_asr_model(dev, enc_layers: int = 24, seed: int = 1):
 
 def e2e_extra(dev, clips: int = 32, seconds: float = 30.0, runs: int = 2):
     """Config 4: 32 clips of 30 s synthetic audio (seeded pink noise + 100-3000 Hz tone bursts at -20 dBFS, dithered
-    as the extractor does) through the whole pipeline -- GPU log-mel, subsampling stem, 24 int8 encoder blocks (2:4
-    feed-forward W2s), projection and cross-attention fill, greedy decoding of up to 448 tokens with continuous
+    as the extractor does) through the whole pipeline -- GPU log-mel, subsampling stem, 24 int8 encoder blocks (both
+    feed-forward linears 2:4), projection and cross-attention fill, greedy decoding of up to 448 tokens with continuous
     batching -- from samples resident on the GPU to token ids. audio-sec/sec = audio seconds / wall seconds of one
     transcribe() call (after a warm-up call)."""
     import numpy as np
@@ -463,11 +573,12 @@ def e2e_extra(dev, clips: int = 32, seconds: float = 30.0, runs: int = 2):
     model = random_asr_model(dev)
     # one encoder call for the whole batch (the reference's 3000-frame chunks keep a service's calls short; here the
     # 32 clips arrive together)
-    pipe = Pipeline(model, slots=clips, max_new_tokens=448, int8=True, sparse=True,
+    pipe = Pipeline(model, None, slots=clips, max_new_tokens=448, int8=True, sparse=True, sparse_w1=True,
                     buckets=(1, 2, 4, 8, 16, 24, 32), chunk_frames=clips * 376)
     setup_s = time.perf_counter() - t0
     n = int(seconds * 16000)
-    pieces = [torch.from_numpy(dither(x)).to(dev) for x in synthetic_audio([n] * clips, seed=7)]
+    host_pieces = [dither(x) for x in synthetic_audio([n] * clips, seed=7)]
+    pieces = [torch.from_numpy(x).to(dev) for x in host_pieces]
     prompt = torch.tensor([4, 5, 6, 7])
     pipe.transcribe(pieces, prompt)  # warm-up
     torch.cuda.synchronize()
@@ -504,7 +615,9 @@ def e2e_extra(dev, clips: int = 32, seconds: float = 30.0, runs: int = 2):
             "walls_s": [round(w, 4) for w in walls], "decode_steps": steps,
             "ms_per_decode_step_upper_bound": round((wall * 1e3 - sum(stage.values())) / max(steps, 1), 4),
             "generated_tokens_mean": float(np.mean(gen)), "encoder_frames": int(sum(lengths)),
-            "stages": stage, "setup_s": round(setup_s, 1)}
+            "stages": stage, "setup_s": round(setup_s, 1),
+            # for the CPU leg's token agreement (removed before printing)
+            "_agreement_inputs": (model, host_pieces[:2], [tokens[0], tokens[1]], prompt.numpy())}
 
 
 def main():
@@ -513,6 +626,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards by data "
               "parallelism with no exchange, and no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
+    # the HBM byte counters, from profiler children started before this process touches the GPU
+    if args.only is None and not args.no_traffic:
+        log("rocprofv3 counter passes for the dominant kernel's traffic")
+    traffic = None if (args.only is not None or args.no_traffic) else measure_traffic()
     import torch
 
     from kernels.cuda_ext import ext
@@ -540,6 +657,7 @@ def main():
     result = {}
 
     if args.only in (None, "step"):
+        log("config-1 step")
         per_graph = 10
         g = graph_of(step, per_graph)
         g1 = graph_of(step, 1)
@@ -562,6 +680,7 @@ def main():
         result.update(ms_per_step=ms, host_ms_per_step=t_host * 1e3 / args.steps)
 
     if args.only in (None, "dominant"):
+        log("dominant kernel")
         # each kernel of the step alone: the dominant one's duration prices the roofline
         reps = 20
         ms_up = time_graph(graph_of(up, reps), 10) / reps
@@ -575,13 +694,15 @@ def main():
                               "ops_per_launch": dom[2], "ms_per_launch": round(dom[1], 5),
                               "note": "int8 TOPS, dense-equivalent (2*M*N*K) against the 2:4 SMFMAC peak"}
         result["kernels_ms"] = {"sparse_up": round(ms_up, 5), "sparse_down": round(ms_dn, 5)}
-        # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary of this command
-        # (FETCH_SIZE + TCC_EA0 write requests, calibrated on a plain copy); null when the profiled kernel differs
-        result["roofline"]["traffic"] = committed_traffic(dom[0])
-        result["roofline"]["traffic_source"] = "profiles/gemm_sp_config1.md (FETCH_SIZE + TCC_EA0 write requests, " \
-                                               "copy-calibrated)"
+        # HBM bytes per launch of the dominant kernel, measured by this run's rocprofv3 passes (null without them)
+        key = "up" if "up" in dom[0] else "down"
+        if traffic is not None:
+            result["roofline"]["traffic"] = traffic[key]["bytes"]
+            result["roofline"]["traffic_detail"] = dict(traffic[key], factors=traffic["factors"],
+                                                        what="rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of this run, "
+                                                             "scaled by a 1 GiB device copy's")
 
-    if args.only == "copy":
+    if args.only in ("copy", "traffic"):
         # calibration for the HBM byte counters: a plain device copy of a known size, 1 GiB read + 1 GiB written,
         # its source evicted from the caches first by writing another 512 MiB
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
@@ -592,8 +713,17 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         result["copy_bytes"] = src.numel()
+        del src, dst, evict
+    if args.only == "traffic":
+        # the GEMMs as profiled: the up projection 3 times, the down projection 5 times (told apart by count)
+        for _ in range(3):
+            up()
+        for _ in range(5):
+            down()
+        torch.cuda.synchronize()
 
     if not args.no_extras and args.only in (None, "dense"):
+        log("config 0 dense")
         def dense():
             d["up_d"](d["xq"], d["xs"], EPI_BIAS, out=up_out)
 
@@ -614,16 +744,21 @@ def main():
         result["dense_config0"]["vendor_int_mm"] = dict(
             what="hipBLASLt via torch._int_mm, dense int8, int32 output only", **vendor)
     if not args.no_extras and args.only in (None, "decoder"):
+        log("config-3 decoder projections")
         result["decoder_gemms"] = decoder_extra(dev)
 
     if not args.no_extras and args.only in (None, "block"):
+        log("config-2 block")
         result["encoder_block"] = block_extra(dev)
     if not args.no_extras and args.only in (None, "decstep"):
+        log("config-3 captured step")
         result["decoder_step"] = decoder_step_extra(dev)
     if not args.no_extras and args.only in (None, "e2e"):
+        log("config-4 end to end")
         result["e2e_config4"] = e2e_extra(dev)
 
     if args.only is not None:
+        result.get("e2e_config4", {}).pop("_agreement_inputs", None)
         print(json.dumps(result))
         return
 
@@ -645,8 +780,16 @@ def main():
     for k in ("dense_config0", "decoder_gemms", "encoder_block", "decoder_step", "e2e_config4"):
         if k in result:
             line[k] = result[k]
+    agreement = line.get("e2e_config4", {}).pop("_agreement_inputs", None)
     if not args.no_cpu:
+        log("CPU baseline (the reference's CPU path)")
         line["cpu_baseline"] = cpu_baseline()
+        if agreement is not None:
+            model, pieces, toks, prompt = agreement
+            log("config 4 through the checker's chain on the CPU (token agreement)")
+            chain_res = cpu_chain(model, pieces, toks, prompt)
+            line["e2e_config4"]["token_agreement"] = chain_res.pop("token_agreement")
+            line["e2e_config4"]["token_agreement_detail"] = chain_res
     print(json.dumps(line))
 
 

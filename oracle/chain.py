@@ -191,16 +191,26 @@ def stem(S: dict, feats: np.ndarray, frames: list[int], threads: int = 0):
     return O.gemm_bf16(a6.reshape(len(a5), -1), S["lin"], S["lin_b"], O.EPI_BIAS, threads=threads), t3
 
 
-def encode(W: dict, pieces: list[np.ndarray], threads: int = 0):
-    """Dithered pieces -> packed encoder output (sum of lengths, 1280) bf16 bits and the lengths."""
+def features(W: dict, pieces: list[np.ndarray], threads: int = 0):
+    """Dithered pieces -> padded log-mel features (B, T, 128) bf16 bits and the frame counts (n // 160 + 1)."""
     m = W["mel"]
     lengths = [len(p) for p in pieces]
     feats = O.logmel(np.concatenate(pieces).astype(np.float32), lengths, m["window"], m["mel"], m["band"],
                      m["preemph"], threads=threads)
-    hidden, t3 = stem(W["stem"], feats, [n // 160 + 1 for n in lengths], threads=threads)
+    return feats, [n // 160 + 1 for n in lengths]
+
+
+def encode_features(W: dict, feats: np.ndarray, frames: list[int], threads: int = 0):
+    """Padded features -> packed encoder output (sum of lengths, 1280) bf16 bits and the lengths."""
+    hidden, t3 = stem(W["stem"], feats, frames, threads=threads)
     run = O.encoder_layers_int8 if W["int8"] else O.encoder_layers_bf16
-    kw = {"threads": threads}
-    return run(hidden, W["layers"], W["eps"], t3, W["rel_off"], W["scale"], **kw), t3
+    return run(hidden, W["layers"], W["eps"], t3, W["rel_off"], W["scale"], threads=threads), t3
+
+
+def encode(W: dict, pieces: list[np.ndarray], threads: int = 0):
+    """Dithered pieces -> packed encoder output (sum of lengths, 1280) bf16 bits and the lengths."""
+    feats, frames = features(W, pieces, threads=threads)
+    return encode_features(W, feats, frames, threads=threads)
 
 
 def decode(W: dict, hidden: np.ndarray, lengths: list[int], prompt, max_new: int, forced_tokens=None,
