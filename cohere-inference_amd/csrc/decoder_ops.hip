@@ -169,42 +169,79 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
 }
 
 template <bool SELF, bool Q8>
-__global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs p) {
+__global__ void __launch_bounds__(AG * 8) __attribute__((amdgpu_waves_per_eu(4)))
+dec_attention_kernel(const DecAttnArgs p) {
+  constexpr int KB = Q8 ? 8 : 4;  // keys per group per pass
+  constexpr int VB = Q8 ? 1 : 2;  // 16-byte value chunks per lane per key
+  // The pass's values are copied global -> LDS by the load unit (global_load_lds), each lane's 16-byte chunks into
+  // its own slots, and read back by the same lane when the softmax weights are known: in flight they hold no
+  // registers, which keeps the kernel at <= 128 VGPRs, two workgroups per CU (one round of 512 workgroups at 64 rows,
+  // where registered values made it two). After the keys the buffer holds the groups' partial outputs.
+  constexpr int VBYTES = KB * VB * 8 * 1024, CBYTES = AG * (HD + 4) * 4;
+  __shared__ __attribute__((aligned(16))) char sbuf[VBYTES > CBYTES ? VBYTES : CBYTES];
   __shared__ float sm[AG], sl[AG], sw[AG], sML[2];
-  __shared__ float sacc[AG][HD + 4];
   __shared__ float spart[4][HD];
+  float(*sacc)[HD + 4] = reinterpret_cast<float(*)[HD + 4]>(sbuf);
   const int r = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
   const int s = p.active[r];
-  const int tid = threadIdx.x, grp = tid >> 3, gl = tid & 7;
+  const int tid = threadIdx.x, grp = tid >> 3, gl = tid & 7, wave = tid >> 6, wl = tid & 63;
   float q[16];
   load16_bf(p.q + (int64_t)r * p.ldq + h * HD + gl * 16, q);
   const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
-  constexpr int KB = Q8 ? 8 : 4;
-  uint4 kr[KB][Q8 ? 1 : 2], vr[KB][Q8 ? 1 : 2];
-  float ksc[KB], vsc[KB];
+  // the wave's LDS block for pass key i, value chunk c (64 lanes x 16 bytes; lane wl's slot at + 16 wl)
+  auto vblock = [&](int i, int c) { return sbuf + ((i * VB + c) * 8 + wave) * 1024; };
+  uint4 kr[KB][Q8 ? 1 : 2];
+  // int8 scales: lane gl of a group loads the scales of the group's key gl of the pass (one load each for the key
+  // and value scales, where one load per key made 16 narrow loads per lane), handed to the group's lanes by index
+  float ksl = 1.f, vsl = 1.f;
+  auto group_lane = [&](float v, int i) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute(((tid & 56) | i) << 2, __float_as_int(v)));
+  };
+  // 32-bit offsets from the layer's cache base (a layer's cache is far below 4 GB), so that the loads take the
+  // uniform base in scalar registers and one offset register each
+  const uint32_t vrow0 = (uint32_t)vec0;
   auto load_pass = [&](int j0, int limit) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const int jj = j0 + i * AG;
-      const int64_t vec = vec0 + (jj < limit ? jj : 0);
+      const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (Q8) {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + vec * HD + gl * 16);
-        vr[i][0] = *reinterpret_cast<const uint4*>(p.v8 + vec * HD + gl * 16);
-        ksc[i] = p.ks[vec];
-        vsc[i] = p.vs[vec];
+        __builtin_amdgcn_global_load_lds(p.v8 + (vec * HD + gl * 16), (LDS_AS void*)vblock(i, 0), 16, 0, 0);
       } else {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16);
-        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + vec * HD + gl * 16 + 8);
-        vr[i][0] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16);
-        vr[i][1] = *reinterpret_cast<const uint4*>(p.v + vec * HD + gl * 16 + 8);
+        const uint16_t* src = p.v + (vec * HD + gl * 16);
+        __builtin_amdgcn_global_load_lds(src, (LDS_AS void*)vblock(i, 0), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(src + 8, (LDS_AS void*)vblock(i, 1), 16, 0, 0);
+      }
+    }
+    if constexpr (Q8) {  // byte offsets in 32 bits: the loads then use the scalar base (one offset register each)
+      const int jj = j0 + gl * AG;
+      const uint32_t off = (vrow0 + (uint32_t)(jj < limit ? jj : 0)) << 2;
+      ksl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.ks) + off);
+      vsl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.vs) + off);
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int jj = j0 + i * AG;
+      const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
+      if constexpr (Q8) {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + (vec * HD + gl * 16));
+      } else {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16));
+        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16 + 8));
       }
     }
   };
-  // cross-attention: the first pass is issued before the slot's length is known (clamped to the cache's T frames,
-  // masked by the length after), so the key loads do not wait for it; the frame count is close to T anyway.
-  // Self-attention lengths grow from 1, so there the length is waited for.
-  const bool early = !SELF && nsp == 1;
-  if (early) load_pass(grp, p.T);
+  auto read_v = [&](int i, float (&vv)[16]) {
+    const uint4 a = *reinterpret_cast<const uint4*>(vblock(i, 0) + wl * 16);
+    if constexpr (Q8) {
+      unpack_q8(a, 1.f, vv);
+    } else {
+      const uint4 b = *reinterpret_cast<const uint4*>(vblock(i, 1) + wl * 16);
+      unpack_bf(a, b, vv);
+    }
+  };
+  // every pass's loads wait for the slot's length (issuing the cross-attention's first pass before it, clamped to
+  // the cache's frames, kept the loaded keys live across the length load and made the kernel spill)
   const int n = p.n[s];
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
@@ -232,8 +269,12 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
   // each group takes KB keys per pass (every 64th key), all loads issued before any use: one memory round trip per
   // pass; then one softmax update for the pass
   int j0 = start + grp;
-  if (!early && j0 < end) load_pass(j0, end);
-  for (; j0 < end; j0 += KB * AG) {
+  // a pass's loads are issued at the top of the pass: no registers carry loaded keys across passes, so one pass of KB
+  // keys per group fits the register budget. Caches of more than KB * AG = 512 keys pay one more memory round trip
+  // per pass.
+  for (bool first = true; j0 < end; j0 += KB * AG, first = false) {
+    if (!first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the last pass's value reads are done
+    load_pass(j0, end);
     float sc[KB], mb = m;
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
@@ -244,28 +285,32 @@ __global__ void __launch_bounds__(AG * 8) dec_attention_kernel(const DecAttnArgs
 #pragma unroll
       for (int k = 0; k < 16; ++k) d = __builtin_fmaf(q[k], kk[k], d);
       d = group_sum(d);
-      if constexpr (Q8) d *= ksc[i];
+      if constexpr (Q8) d *= group_lane(ksl, i);
       sc[i] = j0 + i * AG < end ? d * p.scale : -INFINITY;
       mb = fmaxf(mb, sc[i]);
+      __builtin_amdgcn_sched_barrier(0);  // one key's unpacked values at a time (register pressure)
     }
     const float a = __expf(m - mb);
     l *= a;
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] *= a;
+    // the pass's values have landed in LDS once every load of the wave is done (the value copies were issued first)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const float e = __expf(sc[i] - mb);
       l += e;
       float vv[16];
-      if constexpr (Q8) unpack_q8(vr[i][0], 1.f, vv);  // the integers; the value's scale goes into the weight
-      else unpack_bf(vr[i][0], vr[i][1], vv);
-      const float ew = Q8 ? e * vsc[i] : e;
+      read_v(i, vv);  // int8: the integers; the value's scale goes into the weight
+      const float ew = Q8 ? e * group_lane(vsl, i) : e;
 #pragma unroll
       for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(ew, vv[k], acc[k]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     m = mb;
-    if (j0 + KB * AG < end) load_pass(j0 + KB * AG, end);
   }
+  // every wave is done reading its values before the buffer holds the partial outputs
+  __syncthreads();
   // combine the groups: weights w_g = exp(m_g - M). One wave finds M, the weights and L = sum w_g l_g; then every
   // thread sums 16 groups of one output dimension, and the four partial sums are added in order.
   if (gl == 0) {

@@ -21,7 +21,8 @@ import os
 import torch
 
 _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG, "lib", "libcohere_hip.so")
+# COHERE_HIP_LIBRARY selects another build of the library (A/B comparisons of build options)
+LIB_PATH = os.environ.get("COHERE_HIP_LIBRARY") or os.path.join(_PKG, "lib", "libcohere_hip.so")
 
 EPI_BIAS, EPI_SILU, EPI_RELU, EPI_RESID, EPI_GLU, EPI_SILU_Q8, EPI_CONV_RELU = range(7)
 EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the reference
@@ -418,6 +419,7 @@ class _Ext:
     def _att_checks(self, q, k, out, part, splits):
         _check(k.dim() == 4 and k.shape[3] == 128 and k.is_contiguous() and q.stride(1) == 1 and out.is_contiguous(),
                "dec_attention: caches (slots, H, T, 128) contiguous, q with unit column stride")
+        _check(k.numel() < 2 ** 32, "dec_attention: a cache of 2^32 or more elements (32-bit offsets in the kernel)")
         rows, H = q.shape[0], k.shape[1]
         _check(splits == 1 or (part is not None and part.numel() >= rows * H * splits * 130),
                "dec_attention: splits > 1 needs part")
