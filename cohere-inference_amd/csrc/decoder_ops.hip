@@ -168,16 +168,18 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
   m = mn;
 }
 
-template <bool SELF, bool Q8>
-__global__ void __launch_bounds__(AG * 8) __attribute__((amdgpu_waves_per_eu(4)))
+// LDSV selects where a pass's values wait for the softmax weights: in registers (values loaded with the keys; ~200
+// VGPRs, one 512-thread workgroup per CU) or in LDS, copied global -> LDS by the load unit (global_load_lds), each
+// lane's 16-byte chunks into its own slots and read back by the same lane (<= 128 VGPRs, two workgroups per CU; the
+// copy and read-back add latency). The launch takes LDSV when the grid has more workgroups than the GPU has CUs (64
+// rows x 8 heads: one round of 512 workgroups instead of two), the register form otherwise. After the keys, the LDS
+// buffer holds the groups' partial outputs.
+template <bool SELF, bool Q8, bool LDSV>
+__global__ void __launch_bounds__(AG * 8) __attribute__((amdgpu_waves_per_eu(LDSV ? 4 : 1)))
 dec_attention_kernel(const DecAttnArgs p) {
   constexpr int KB = Q8 ? 8 : 4;  // keys per group per pass
   constexpr int VB = Q8 ? 1 : 2;  // 16-byte value chunks per lane per key
-  // The pass's values are copied global -> LDS by the load unit (global_load_lds), each lane's 16-byte chunks into
-  // its own slots, and read back by the same lane when the softmax weights are known: in flight they hold no
-  // registers, which keeps the kernel at <= 128 VGPRs, two workgroups per CU (one round of 512 workgroups at 64 rows,
-  // where registered values made it two). After the keys the buffer holds the groups' partial outputs.
-  constexpr int VBYTES = KB * VB * 8 * 1024, CBYTES = AG * (HD + 4) * 4;
+  constexpr int VBYTES = LDSV ? KB * VB * 8 * 1024 : 0, CBYTES = AG * (HD + 4) * 4;
   __shared__ __attribute__((aligned(16))) char sbuf[VBYTES > CBYTES ? VBYTES : CBYTES];
   __shared__ float sm[AG], sl[AG], sw[AG], sML[2];
   __shared__ float spart[4][HD];
@@ -188,24 +190,31 @@ dec_attention_kernel(const DecAttnArgs p) {
   float q[16];
   load16_bf(p.q + (int64_t)r * p.ldq + h * HD + gl * 16, q);
   const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
-  // the wave's LDS block for pass key i, value chunk c (64 lanes x 16 bytes; lane wl's slot at + 16 wl)
+  // LDSV: the wave's LDS block for pass key i, value chunk c (64 lanes x 16 bytes; lane wl's slot at + 16 wl)
   auto vblock = [&](int i, int c) { return sbuf + ((i * VB + c) * 8 + wave) * 1024; };
-  uint4 kr[KB][Q8 ? 1 : 2];
+  uint4 kr[KB][Q8 ? 1 : 2], vr[LDSV ? 1 : KB][Q8 ? 1 : 2];
   // int8 scales: lane gl of a group loads the scales of the group's key gl of the pass (one load each for the key
   // and value scales, where one load per key made 16 narrow loads per lane), handed to the group's lanes by index
   float ksl = 1.f, vsl = 1.f;
   auto group_lane = [&](float v, int i) {
     return __int_as_float(__builtin_amdgcn_ds_bpermute(((tid & 56) | i) << 2, __float_as_int(v)));
   };
-  // 32-bit offsets from the layer's cache base (a layer's cache is far below 4 GB), so that the loads take the
-  // uniform base in scalar registers and one offset register each
+  // 32-bit offsets from the layer's cache base (a layer's cache stays below 2^32 elements), so that the loads take
+  // the uniform base in scalar registers and one offset register each
   const uint32_t vrow0 = (uint32_t)vec0;
   auto load_pass = [&](int j0, int limit) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
-      if constexpr (Q8) {
+      if constexpr (!LDSV) {
+        if constexpr (Q8) {
+          vr[i][0] = *reinterpret_cast<const uint4*>(p.v8 + (vec * HD + gl * 16));
+        } else {
+          vr[i][0] = *reinterpret_cast<const uint4*>(p.v + (vec * HD + gl * 16));
+          vr[i][1] = *reinterpret_cast<const uint4*>(p.v + (vec * HD + gl * 16 + 8));
+        }
+      } else if constexpr (Q8) {
         __builtin_amdgcn_global_load_lds(p.v8 + (vec * HD + gl * 16), (LDS_AS void*)vblock(i, 0), 16, 0, 0);
       } else {
         const uint16_t* src = p.v + (vec * HD + gl * 16);
@@ -232,16 +241,23 @@ dec_attention_kernel(const DecAttnArgs p) {
     }
   };
   auto read_v = [&](int i, float (&vv)[16]) {
-    const uint4 a = *reinterpret_cast<const uint4*>(vblock(i, 0) + wl * 16);
-    if constexpr (Q8) {
-      unpack_q8(a, 1.f, vv);
+    uint4 a, b;
+    if constexpr (LDSV) {
+      a = *reinterpret_cast<const uint4*>(vblock(i, 0) + wl * 16);
+      if constexpr (!Q8) b = *reinterpret_cast<const uint4*>(vblock(i, 1) + wl * 16);
     } else {
-      const uint4 b = *reinterpret_cast<const uint4*>(vblock(i, 1) + wl * 16);
-      unpack_bf(a, b, vv);
+      a = vr[i][0];
+      if constexpr (!Q8) b = vr[i][1];
     }
+    if constexpr (Q8) unpack_q8(a, 1.f, vv);
+    else unpack_bf(a, b, vv);
   };
-  // every pass's loads wait for the slot's length (issuing the cross-attention's first pass before it, clamped to
-  // the cache's frames, kept the loaded keys live across the length load and made the kernel spill)
+  // register form, cross-attention: the first pass is issued before the slot's length is known (clamped to the
+  // cache's T frames, masked by the length after), so the key loads do not wait for it; the frame count is close to
+  // T anyway. Self-attention lengths grow from 1, so there the length is waited for. (In the LDS form the early pass
+  // kept the loaded keys live across the length load and made the kernel spill.)
+  const bool early = !LDSV && !SELF && nsp == 1;
+  if (early) load_pass(grp, p.T);
   const int n = p.n[s];
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
@@ -273,8 +289,10 @@ dec_attention_kernel(const DecAttnArgs p) {
   // keys per group fits the register budget. Caches of more than KB * AG = 512 keys pay one more memory round trip
   // per pass.
   for (bool first = true; j0 < end; j0 += KB * AG, first = false) {
-    if (!first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the last pass's value reads are done
-    load_pass(j0, end);
+    if (!(first && early)) {
+      if (LDSV && !first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
+      load_pass(j0, end);
+    }
     float sc[KB], mb = m;
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
@@ -294,8 +312,8 @@ dec_attention_kernel(const DecAttnArgs p) {
     l *= a;
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] *= a;
-    // the pass's values have landed in LDS once every load of the wave is done (the value copies were issued first)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // LDSV: the pass's values have landed in LDS once every load of the wave is done (the copies were issued first)
+    if constexpr (LDSV) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const float e = __expf(sc[i] - mb);
@@ -309,8 +327,12 @@ dec_attention_kernel(const DecAttnArgs p) {
     }
     m = mb;
   }
-  // every wave is done reading its values before the buffer holds the partial outputs
-  __syncthreads();
+  // LDSV: every wave is done reading its values (and an early pass has landed) before the buffer holds the partial
+  // outputs
+  if constexpr (LDSV) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
   // combine the groups: weights w_g = exp(m_g - M). One wave finds M, the weights and L = sum w_g l_g; then every
   // thread sums 16 groups of one output dimension, and the four partial sums are added in order.
   if (gl == 0) {
@@ -556,6 +578,17 @@ extern "C" int cohere_dec_add_ln(uint16_t* x, const uint16_t* y, int64_t ldy, co
 }
 
 namespace {
+int num_cus() {
+  static const int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || v <= 0)
+      v = 256;
+    return v;
+  }();
+  return n;
+}
+
 int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t splits, int64_t part_len,
                     void* stream, const char* name) {
   const std::string nm(name);
@@ -569,13 +602,13 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
   if (rows == 0) return 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)rows, (unsigned)p.H, (unsigned)splits);
-  if (self) {
-    if (q8) dec_attention_kernel<true, true><<<grid, AG * 8, 0, s>>>(p);
-    else dec_attention_kernel<true, false><<<grid, AG * 8, 0, s>>>(p);
-  } else {
-    if (q8) dec_attention_kernel<false, true><<<grid, AG * 8, 0, s>>>(p);
-    else dec_attention_kernel<false, false><<<grid, AG * 8, 0, s>>>(p);
-  }
+  const bool ldsv = rows * p.H * splits > num_cus();
+#define COHERE_ATT(SELF_, Q8_)                                                                    \
+  (ldsv ? (dec_attention_kernel<SELF_, Q8_, true><<<grid, AG * 8, 0, s>>>(p), 0)                  \
+        : (dec_attention_kernel<SELF_, Q8_, false><<<grid, AG * 8, 0, s>>>(p), 0))
+  if (self) q8 ? COHERE_ATT(true, true) : COHERE_ATT(true, false);
+  else q8 ? COHERE_ATT(false, true) : COHERE_ATT(false, false);
+#undef COHERE_ATT
   if (splits > 1) dec_combine_kernel<<<dim3((unsigned)rows, (unsigned)p.H), HD, 0, s>>>(p.part, (int)splits, p.out, p.H);
   return cohere::check_launch(name);
 }

@@ -401,13 +401,32 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
   // Dense: the freed buffer's next transfer is issued after the step's matrix instructions (flush_issue), so that a
   // busy load unit never holds up the matrix cores at the start of a step (measured: 5 % faster dense loops; the
   // sparse tiles, with one step per stage, are faster issuing at once).
+  // LAG2 (double-buffered fragments and at least 4 stages): entering stage t frees stage t - 2, not t - 1. A wave
+  // then still has the previous step's fragment reads (from stage t - 1) in flight at the barrier, and the barrier
+  // does not wait for them (lgkmcnt), so those reads overlap the matrix instructions; the DMA runs ST - 2 stages
+  // ahead instead of ST - 1.
+  constexpr bool LAG2 = T::PF && ST >= 4;
+  constexpr int AHEAD = LAG2 ? ST - 2 : ST - 1;  // stages in flight beyond the one being waited for, at most
   int pending = -1;
   auto enter_stage = [&](int t) {
-    wait_stages<LPS, ST>(min(KT - 1 - t, ST - 2));
-    lds_barrier();
-    if (t - 1 + ST < KT) {
-      if constexpr (SPARSE) issue((t - 1 + ST) % ST, t - 1 + ST);
-      else pending = t - 1 + ST;
+    wait_stages<LPS, ST>(min(KT - 1 - t, AHEAD - 1));
+    if constexpr (LAG2) asm volatile("s_barrier" ::: "memory");
+    else lds_barrier();
+    const int next = t + AHEAD;
+    if (next < KT) {
+      if constexpr (SPARSE) issue(next % ST, next);
+      else pending = next;
+    }
+  };
+  // the step's matrix instructions interleaved with the next step's fragment reads (scheduling hints only)
+  auto interleave = [&]() {
+    constexpr int NMFMA = MI * NI;
+    constexpr int NREAD = SPARSE ? 2 * MI + 2 * NI : MI + NI;
+    constexpr int PER = (NREAD + NMFMA - 1) / NMFMA;
+#pragma unroll
+    for (int k = 0; k < NMFMA; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // one matrix instruction
+      __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);  // then up to PER LDS reads
     }
   };
   auto flush_issue = [&]() {
@@ -426,9 +445,9 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       for (int c = tid; c < BN / 2; c += NT) reinterpret_cast<uint32_t*>(pBh)[c] = 0x80008000u;
   }
 #pragma unroll
-  for (int s = 1; s < ST; ++s)
+  for (int s = 1; s <= AHEAD; ++s)
     if (s < KT) issue(s, s);
-  wait_stages<LPS, ST>(min(KT - 1, ST - 1));
+  wait_stages<LPS, ST>(min(KT - 1, AHEAD));
   lds_barrier();
   if constexpr (GS > 0) {
     // whole groups of GS steps, unrolled: the fold sits at each group's first step (not the first group's), so the
@@ -467,10 +486,12 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       if ((u + 1) % SPS == 0) enter_stage((u + 1) / SPS);
       load_frags(F1, u + 1);
       mma(F0);
+      if constexpr (!GROUPED) interleave();
       flush_issue();
       if ((u + 2) % SPS == 0) enter_stage((u + 2) / SPS);
       load_frags(F0, u + 2);
       mma(F1);
+      if constexpr (!GROUPED) interleave();
       flush_issue();
     }
     if (u + 1 < NSTEPS) {
