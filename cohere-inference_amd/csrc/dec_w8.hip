@@ -21,20 +21,30 @@
 //    accepted (and checked as it checks them) but not needed.
 #include "common.h"
 #include "cohere_hip.h"
+#include "rows.h"
 
 #include <string>
 
 namespace {
 
 struct SkinnyArgs {
-  const uint16_t* X;  // [M, K] bf16
+  const uint16_t* X;  // [M, K] bf16 (with a LayerNorm prologue: the residual stream before the norm)
   const void* W;      // uint8 [N, K] (prepare_w8) or bf16 [N, K]
   const float* sw;    // [N] (int8 weights only)
   const uint16_t* bias;
-  uint16_t* Y;        // [M, N]
+  uint16_t* Y;        // [M, N] (residual epilogue: read and updated in place)
+  const uint16_t* lnw;  // LayerNorm prologue weight and bias [K] (null: X is the GEMM input as it is)
+  const uint16_t* lnb;
+  float eps;
   int64_t ldx, ldy;
   int M, N, K;
 };
+
+// epilogues
+enum { EP_NONE = 0, EP_RELU = 1, EP_RESID = 2 };
+constexpr int LN_K = 1024;           // widest LayerNorm prologue (the rows are held in LDS)
+constexpr int LN_ROW = LN_K * 2 + 16;  // LDS bytes per normalised row (16 bytes of padding: conflict-free reads)
+
 
 constexpr int KB = 64;  // K per block
 
@@ -58,11 +68,16 @@ DEVI v8bf as_bf8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return __builtin_bit_cast(v8bf, v);
 }
 
-template <int MB, int NS, int NW, bool W8, bool RELU>
+// MB row blocks of 16, NS strips of 16 channels, NW waves; EP the epilogue; LN: the rows are LayerNormed first (one
+// wave per row, the same arithmetic as dec_add_ln) into LDS, and the K loop reads its activations from there
+template <int MB, int NS, int NW, bool W8, int EP, bool LN>
 __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   constexpr int MAXB = (W8 ? 16 : 8) / NS;  // K blocks per wave held in registers at once (64 VGPRs of weights)
   constexpr int COLS = NS * 16, LDR = COLS + 4;
-  __shared__ __attribute__((aligned(16))) float red[NW][MB * 16][LDR];
+  constexpr int RED = NW * MB * 16 * LDR * 4, XS = LN ? MB * 16 * LN_ROW : 0;
+  // the waves' partial tiles (after the K loop) share LDS with the normalised rows (during it)
+  __shared__ __attribute__((aligned(16))) char smem[RED > XS ? RED : XS];
+  auto red = reinterpret_cast<float (*)[MB * 16][LDR]>(smem);
   const int n0 = blockIdx.x * COLS, m_base = blockIdx.y * MB * 16;  // grid.y > 1: the rows split over workgroups
   const int lane = threadIdx.x & 63, wave = wave_id(), h = lane >> 4, c16 = lane & 15;
   const int nkb = p.K / KB;  // wave w takes blocks w, w + NW, ...
@@ -81,6 +96,22 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   const uint16_t* bsrc = p.bias ? p.bias : static_cast<const uint16_t*>(p.W);
   const uint16_t b_ep = bsrc[n_ep];
 
+  // LayerNorm prologue: each wave's rows (two loaded before the weights, so that only they are waited for ahead of
+  // the weights; the rest, with MB > 1, after)
+  constexpr int RPW = LN ? MB * 16 / NW : 1, PRE = RPW < 2 ? RPW : 2;
+  static_assert(!LN || (MB * 16) % NW == 0, "rows per wave");
+  cohere_rows::Row<2> rows_pre[PRE];
+  cohere_rows::LnParams<2> lnp;
+  if constexpr (LN) {
+    lnp = cohere_rows::load_ln<2>(p.lnw, p.lnb, p.K, lane);
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) {
+      const int m = min(m_base + wave * RPW + j, p.M - 1);
+      cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j]);
+    }
+  }
+
+  bool first = true;
   for (int b0 = wave; b0 < nkb; b0 += NW * MAXB) {
     uint4 wreg[MAXB][NS][W8 ? 1 : 2];
 #pragma unroll
@@ -99,6 +130,25 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
             wreg[b][s][1] = *reinterpret_cast<const uint4*>(wr + 32 + 8 * h);
           }
         }
+      }
+    }
+    if constexpr (LN) {
+      if (first) {
+        // every wave reaches this (the caller guarantees at least NW blocks of K)
+#pragma unroll
+        for (int j = 0; j < RPW; ++j) {
+          cohere_rows::Row<2> r;
+          if (j < PRE) {
+            r = rows_pre[j];
+          } else {
+            const int m = min(m_base + wave * RPW + j, p.M - 1);
+            cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, r);
+          }
+          cohere_rows::ln_row<2>(r, p.K, lane, lnp, p.eps);
+          cohere_rows::store_row<2>(r, p.K, lane, reinterpret_cast<uint16_t*>(smem + (wave * RPW + j) * LN_ROW));
+        }
+        __syncthreads();
+        first = false;
       }
     }
 #pragma unroll
@@ -120,8 +170,13 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const int m = min(m_base + mb * 16 + c16, p.M - 1);
-        const uint16_t* xr = p.X + (int64_t)m * p.ldx + k;
+        const uint16_t* xr;
+        if constexpr (LN) {
+          xr = reinterpret_cast<const uint16_t*>(smem + (mb * 16 + c16) * LN_ROW) + k;
+        } else {
+          const int m = min(m_base + mb * 16 + c16, p.M - 1);
+          xr = p.X + (int64_t)m * p.ldx + k;
+        }
         v8bf x0, x1;
         if constexpr (W8) {
           const uint4 lo = *reinterpret_cast<const uint4*>(xr + 16 * h);      // logical 0..7 of this 16-block
@@ -144,6 +199,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   }
 
   // the waves' partial tiles, summed in wave order
+  if constexpr (LN) __syncthreads();  // every wave is done reading the normalised rows
 #pragma unroll
   for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -158,45 +214,58 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
     for (int w = 1; w < NW; ++w) v += red[w][r][c];
     if constexpr (W8) v = __builtin_fmaf(v, sw_ep, p.bias ? bf2f(b_ep) : 0.f);
     else if (p.bias) v = v + bf2f(b_ep);
-    if (RELU) v = fmaxf(v, 0.f);
-    p.Y[(int64_t)m * p.ldy + n0 + c] = f2bf(v);
+    if constexpr (EP == EP_RELU) v = fmaxf(v, 0.f);
+    uint16_t* y = p.Y + (int64_t)m * p.ldy + n0 + c;
+    // residual: y = bf16(y + bf16(v)), dec_add_ln's sum
+    if constexpr (EP == EP_RESID) v = bf2f(*y) + round_bf(v);
+    *y = f2bf(v);
   }
 }
 
 int g_skinny_override = -1;  // (NS << 8) | NW, tuning hook
 
-template <int NS, int NW, bool W8, bool RELU>
+template <int NS, int NW, bool W8, int EP, bool LN>
 void launch_rows(const SkinnyArgs& p, hipStream_t s) {
   const int grid = p.N / (NS * 16), mblocks = (p.M + 15) / 16;
   if (grid * mblocks <= 512 && mblocks > 1) {
     // few channel strips: one workgroup per (strip, 16 rows), so that every CU streams (the strip is read once per
     // 16 rows, the repeats mostly from L2 / MALL)
-    skinny_kernel<1, NS, NW, W8, RELU><<<dim3(grid, mblocks), NW * 64, 0, s>>>(p);
+    skinny_kernel<1, NS, NW, W8, EP, LN><<<dim3(grid, mblocks), NW * 64, 0, s>>>(p);
     return;
   }
   switch (mblocks) {
-    case 1: skinny_kernel<1, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
-    case 2: skinny_kernel<2, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
-    case 3: skinny_kernel<3, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
-    default: skinny_kernel<4, NS, NW, W8, RELU><<<grid, NW * 64, 0, s>>>(p); break;
+    case 1: skinny_kernel<1, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
+    case 2: skinny_kernel<2, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
+    case 3: skinny_kernel<3, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
+    default: skinny_kernel<4, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
   }
 }
 
-template <bool W8, bool RELU>
+template <bool W8, int EP, bool LN>
 int launch_shape(int ns, int nw, const SkinnyArgs& p, hipStream_t s) {
   const int key = (ns << 8) | nw;
-  switch (key) {
-    case (1 << 8) | 16: launch_rows<1, 16, W8, RELU>(p, s); break;
-    case (1 << 8) | 8: launch_rows<1, 8, W8, RELU>(p, s); break;
-    case (1 << 8) | 4: launch_rows<1, 4, W8, RELU>(p, s); break;
-    case (2 << 8) | 8: launch_rows<2, 8, W8, RELU>(p, s); break;
-    case (2 << 8) | 4: launch_rows<2, 4, W8, RELU>(p, s); break;
-    case (4 << 8) | 8: launch_rows<4, 8, W8, RELU>(p, s); break;
-    case (4 << 8) | 4: launch_rows<4, 4, W8, RELU>(p, s); break;
-    default: cohere::set_error("skinny: no kernel for ns=" + std::to_string(ns) + " nw=" + std::to_string(nw));
-             return 1;
+  if constexpr (LN || EP == EP_RESID) {
+    // the fused forms: eight waves
+    switch (key) {
+      case (1 << 8) | 8: launch_rows<1, 8, W8, EP, LN>(p, s); return 0;
+      case (2 << 8) | 8: launch_rows<2, 8, W8, EP, LN>(p, s); return 0;
+      case (4 << 8) | 8: launch_rows<4, 8, W8, EP, LN>(p, s); return 0;
+      default: break;
+    }
+  } else {
+    switch (key) {
+      case (1 << 8) | 16: launch_rows<1, 16, W8, EP, LN>(p, s); return 0;
+      case (1 << 8) | 8: launch_rows<1, 8, W8, EP, LN>(p, s); return 0;
+      case (1 << 8) | 4: launch_rows<1, 4, W8, EP, LN>(p, s); return 0;
+      case (2 << 8) | 8: launch_rows<2, 8, W8, EP, LN>(p, s); return 0;
+      case (2 << 8) | 4: launch_rows<2, 4, W8, EP, LN>(p, s); return 0;
+      case (4 << 8) | 8: launch_rows<4, 8, W8, EP, LN>(p, s); return 0;
+      case (4 << 8) | 4: launch_rows<4, 4, W8, EP, LN>(p, s); return 0;
+      default: break;
+    }
   }
-  return 0;
+  cohere::set_error("skinny: no kernel for ns=" + std::to_string(ns) + " nw=" + std::to_string(nw));
+  return 1;
 }
 
 // channels per workgroup (strips of 16) and waves per workgroup, measured on MI355X for the decoder's shapes (graph
@@ -218,19 +287,38 @@ void choose_shape(int N, int K, int M, int& ns, int& nw) {
 
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; }
 
-int skinny_entry(SkinnyArgs& p, bool w8, int relu, hipStream_t s, const char* name) {
+int skinny_entry(SkinnyArgs& p, bool w8, int ep, hipStream_t s, const char* name) {
   const std::string nm(name);
   COHERE_REQUIRE(p.M >= 0 && p.M <= 64, nm + ": at most 64 rows per call (got " + std::to_string(p.M) + ")");
   COHERE_REQUIRE(p.N > 0 && p.N % 16 == 0, nm + ": N must be a multiple of 16");
   COHERE_REQUIRE(p.K > 0 && p.K % KB == 0, nm + ": K must be a multiple of 64");
   COHERE_REQUIRE(p.X && p.W && p.Y && (!w8 || p.sw), nm + ": null pointer");
   COHERE_REQUIRE(al16(p.X) && p.ldx % 8 == 0 && al16(p.W), nm + ": x rows and weights must be 16-byte aligned");
+  COHERE_REQUIRE(ep >= EP_NONE && ep <= EP_RESID, nm + ": unknown epilogue " + std::to_string(ep));
+  const bool ln = p.lnw != nullptr;
+  COHERE_REQUIRE(!ln || (p.lnb && p.K >= 8 * KB && p.K <= LN_K && al16(p.lnw) && al16(p.lnb)),
+                 nm + ": a LayerNorm prologue takes 512 <= K <= 1024 (got " + std::to_string(p.K) +
+                     ") and 16-byte aligned weight and bias");
   if (p.M == 0) return 0;
   int ns, nw;
   choose_shape(p.N, p.K, p.M, ns, nw);
+  if (ln || ep == EP_RESID) nw = 8;
   int rc;
-  if (w8) rc = relu ? launch_shape<true, true>(ns, nw, p, s) : launch_shape<true, false>(ns, nw, p, s);
-  else rc = relu ? launch_shape<false, true>(ns, nw, p, s) : launch_shape<false, false>(ns, nw, p, s);
+  if (ln) {
+    if (ep == EP_RESID) rc = 1, cohere::set_error(nm + ": no residual epilogue after a LayerNorm prologue");
+    else if (w8) rc = ep == EP_RELU ? launch_shape<true, EP_RELU, true>(ns, nw, p, s)
+                                    : launch_shape<true, EP_NONE, true>(ns, nw, p, s);
+    else rc = ep == EP_RELU ? launch_shape<false, EP_RELU, true>(ns, nw, p, s)
+                            : launch_shape<false, EP_NONE, true>(ns, nw, p, s);
+  } else if (ep == EP_RESID) {
+    rc = w8 ? launch_shape<true, EP_RESID, false>(ns, nw, p, s) : launch_shape<false, EP_RESID, false>(ns, nw, p, s);
+  } else if (w8) {
+    rc = ep == EP_RELU ? launch_shape<true, EP_RELU, false>(ns, nw, p, s)
+                       : launch_shape<true, EP_NONE, false>(ns, nw, p, s);
+  } else {
+    rc = ep == EP_RELU ? launch_shape<false, EP_RELU, false>(ns, nw, p, s)
+                       : launch_shape<false, EP_NONE, false>(ns, nw, p, s);
+  }
   if (rc) return rc;
   return cohere::check_launch(name);
 }
@@ -252,7 +340,7 @@ extern "C" int cohere_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_
   SkinnyArgs p{};
   p.X = x; p.W = w; p.sw = sw; p.bias = bias; p.Y = y;
   p.ldx = ldx; p.ldy = ldy; p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  return skinny_entry(p, true, relu, reinterpret_cast<hipStream_t>(stream), "dec_w8_linear");
+  return skinny_entry(p, true, relu ? EP_RELU : EP_NONE, reinterpret_cast<hipStream_t>(stream), "dec_w8_linear");
 }
 
 extern "C" int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias,
@@ -262,7 +350,17 @@ extern "C" int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t
   SkinnyArgs p{};
   p.X = x; p.W = w; p.sw = nullptr; p.bias = bias; p.Y = y;
   p.ldx = ldx; p.ldy = ldy; p.M = (int)M; p.N = (int)N; p.K = (int)K;
-  return skinny_entry(p, false, relu, reinterpret_cast<hipStream_t>(stream), "linear_bf16");
+  return skinny_entry(p, false, relu ? EP_RELU : EP_NONE, reinterpret_cast<hipStream_t>(stream), "linear_bf16");
+}
+
+extern "C" int cohere_dec_linear_fused(const uint16_t* x, int64_t ldx, const uint16_t* ln_w, const uint16_t* ln_b,
+                                       float eps, const void* w, const float* sw, const uint16_t* bias, uint16_t* y,
+                                       int64_t ldy, int32_t epilogue, int64_t M, int64_t N, int64_t K, void* stream) {
+  cohere::clear_error();
+  SkinnyArgs p{};
+  p.X = x; p.W = w; p.sw = sw; p.bias = bias; p.Y = y; p.lnw = ln_w; p.lnb = ln_b; p.eps = eps;
+  p.ldx = ldx; p.ldy = ldy; p.M = (int)M; p.N = (int)N; p.K = (int)K;
+  return skinny_entry(p, sw != nullptr, epilogue, reinterpret_cast<hipStream_t>(stream), "dec_linear_fused");
 }
 
 extern "C" int cohere_set_skinny_shape(int32_t strips, int32_t waves) {

@@ -25,6 +25,7 @@ _PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("COHERE_HIP_LIBRARY") or os.path.join(_PKG, "lib", "libcohere_hip.so")
 
 EPI_BIAS, EPI_SILU, EPI_RELU, EPI_RESID, EPI_GLU, EPI_SILU_Q8, EPI_CONV_RELU = range(7)
+DEC_EP_NONE, DEC_EP_RELU, DEC_EP_RESID = range(3)  # dec_linear_fused's epilogues
 EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the reference
 
 # every symbol include/cohere_hip.h declares
@@ -35,7 +36,7 @@ EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_l
            "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
            "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8", "cohere_gemm_bf16", "cohere_logmel_workspace_bytes",
            "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw", "cohere_encoder_branch_workspace_bytes",
-           "cohere_encoder_layers_noalloc")
+           "cohere_encoder_layers_noalloc", "cohere_dec_linear_fused")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -51,6 +52,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_layernorm_q8": [P, I64, P, P, F, P, P, F, P, I64, P, I64, I64, P],
         "cohere_dec_w8_linear": [P, I64, P, P, P, P, I64, I32, I64, I64, P, I64, P, I64, I64, I64, I64, P],
         "cohere_linear_bf16": [P, I64, P, P, P, I64, I32, I64, I64, I64, P],
+        "cohere_dec_linear_fused": [P, I64, P, P, F, P, P, P, P, I64, I32, I64, I64, I64, P],
         "cohere_set_gemm_tile": [I32],
         "cohere_set_skinny_shape": [I32, I32],
         "cohere_layernorm": [P, I64, P, P, F, P, P, F, P, I64, I64, I64, P],
@@ -395,6 +397,22 @@ class _Ext:
         self._call("cohere_linear_bf16", _ptr(x), x.stride(0), _ptr(w), _ptr(bias), _ptr(y), y.stride(0),
                    int(bool(relu)), M, w.shape[0], K, _stream())
 
+    def dec_linear_fused(self, x, w, sw, bias, y, epilogue=DEC_EP_NONE, ln=None):
+        """A decoder projection with dec_add_ln folded in (no single counterpart in the reference, whose step runs
+        dec_add_ln between the projections, stream_decoder.py:176-199): ln = (weight, bias, eps) normalises x's rows
+        in the kernel first (512 <= K <= 1024); epilogue DEC_EP_RELU applies ReLU, DEC_EP_RESID adds the result into
+        y in place (y = bf16(y + bf16(r))). sw None: bf16 weights w; else int8 weights in prepare_w8's layout."""
+        _check(x.dtype == torch.bfloat16 and y.dtype == torch.bfloat16 and
+               (w.dtype == torch.uint8 if sw is not None else w.dtype == torch.bfloat16), "dec_linear_fused: dtypes")
+        M, K = x.shape
+        _check(M <= 64 and x.stride(1) == 1 and w.is_contiguous() and w.shape[1] == K and y.stride(1) == 1 and
+               y.shape[0] == M and y.shape[1] == w.shape[0], "dec_linear_fused: M <= 64, unit column strides, "
+               "contiguous w, y (M, N)")
+        if M == 0:
+            return
+        lw, lb, eps = ln if ln is not None else (None, None, 0.0)
+        self._call("cohere_dec_linear_fused", _ptr(x), x.stride(0), _ptr(lw), _ptr(lb), float(eps), _ptr(w),
+                   _ptr(sw), _ptr(bias), _ptr(y), y.stride(0), int(epilogue), M, w.shape[0], K, _stream())
 
     # ---- decoder step (bindings.cpp:77-84) -------------------------------------------------------------------------
 

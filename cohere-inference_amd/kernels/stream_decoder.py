@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import torch
 
-from kernels.cuda_ext import ext
+from kernels.cuda_ext import DEC_EP_NONE, DEC_EP_RELU, DEC_EP_RESID, ext
 
 # (N, K) -> {rows up to: (columns per CTA, K splits)}: the reference's A10 table, accepted for compatibility. The gfx950
 # kernel checks these like the reference does and then chooses its own tiling (results never depend on it).
@@ -112,6 +112,12 @@ class _Projection:
                 bn, _ = w8_config(self.n, self.k, xr.shape[0])
                 ext.dec_w8_linear(xr, self.weight, self.scale, self.bias, yr, relu, bn, 1, None, None)
 
+    def fused(self, x: torch.Tensor, y: torch.Tensor, epilogue: int = DEC_EP_NONE, ln=None) -> None:
+        """The projection with its neighbouring residual LayerNorm folded in (ext.dec_linear_fused): ln normalises
+        x's rows first; DEC_EP_RESID adds the result into y (the residual stream) in place."""
+        for r in range(0, x.shape[0], 64):
+            ext.dec_linear_fused(x[r:r + 64], self.weight, self.scale, self.bias, y[r:r + 64], epilogue, ln)
+
 
 class _Block:
     """One decoder layer: its three LayerNorms (weight, bias, eps) and six projections. With int8, the
@@ -146,7 +152,7 @@ class StreamDecoder:
 
     def __init__(self, model, slots: int = 128, max_new_tokens: int = 448, max_prompt: int = 16,
                  max_audio_s: float = 36.0, buckets=None, int8: bool = False, frames: int | None = None,
-                 capture: bool = True):
+                 capture: bool = True, fused: bool | None = None):
         dec, cfg = model.model.decoder, model.config
         self.model, self.int8 = model, int8
         self.buckets = tuple(sorted(b for b in (buckets or self.BUCKETS) if b <= slots))
@@ -164,6 +170,12 @@ class StreamDecoder:
             frames = int(model.model.encoder._get_subsampling_output_length(
                 torch.tensor([int(max_audio_s * 100) + 1])).item())
         self.frames = frames
+        # residual LayerNorms folded into the projections (ext.dec_linear_fused) where its prologue takes the width;
+        # fused=False keeps the reference's separate dec_add_ln launches (the same bits)
+        can_fuse = 512 <= self.width <= 1024 and self.width % 64 == 0
+        if fused and not can_fuse:
+            raise ValueError(f"StreamDecoder: fused projections take widths 512-1024 (got {self.width})")
+        self.fused = can_fuse if fused is None else bool(fused)
 
         # weights
         self.embed, self.pos_table = dec.embed_tokens.weight, dec.pos_emb.weight
@@ -254,6 +266,25 @@ class StreamDecoder:
                                                      self.logits))
         ops = [lambda: ext.dec_embed(act, self.tok, self.pos, self.embed, self.pos_table, *self.emb_ln,
                                      *self.blocks[0].norms[0], x, hn)]
+        if self.fused:
+            # the residual adds ride on o / cross-o / fc2's epilogues and the LayerNorms on the next projection's
+            # prologue: 8 launches a layer instead of 11, the same bits
+            for i, blk in enumerate(self.blocks):
+                first = i == 0
+                ops += [(lambda blk=blk: blk.qkv.fused(hn, qkv)) if first else
+                        (lambda blk=blk: blk.qkv.fused(x, qkv, ln=blk.norms[0])),
+                        self._attention(i, True, act, qkv, 1, att),
+                        lambda blk=blk: blk.o.fused(att, x, DEC_EP_RESID),
+                        lambda blk=blk: blk.cq.fused(x, q, ln=blk.norms[1]),
+                        self._attention(i, False, act, q, self._splits(b), att),
+                        lambda blk=blk: blk.co.fused(att, x, DEC_EP_RESID),
+                        lambda blk=blk: blk.fc1.fused(x, ffn, DEC_EP_RELU, ln=blk.norms[2]),
+                        lambda blk=blk: blk.fc2.fused(ffn, x, DEC_EP_RESID)]
+            ops += [lambda: self.head.fused(x, logits, ln=self.final_ln),
+                    lambda: ext.dec_pick(logits, act, self.dummy, self.tok, self.pos, self.finished, self.forced,
+                                         self.plen, self.limit, self.out, self.pad, self.eos),
+                    lambda: self.flags.copy_(self.finished, non_blocking=True)]
+            return ops
         for i, blk in enumerate(self.blocks):
             after_ffn = self.blocks[i + 1].norms[0] if i + 1 < len(self.blocks) else self.final_ln
             ops += [lambda blk=blk: blk.qkv(hn, qkv),

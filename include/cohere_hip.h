@@ -105,6 +105,20 @@ int cohere_dec_w8_linear(const uint16_t* x, int64_t ldx, const uint8_t* w, const
 int cohere_linear_bf16(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* bias, uint16_t* y,
                        int64_t ldy, int32_t relu, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* No single counterpart in the reference: its decoder step (kernels/stream_decoder.py:176-199) runs
+ * dec_add_ln (kernels/csrc/decoder_ops.cu:56-83) between the projections; this entry point folds that LayerNorm and
+ * residual add into the projections around it, so that a step has three launches per layer fewer. With the same
+ * arithmetic as dec_add_ln followed by dec_w8_linear / linear_bf16, its results are bit-identical to theirs.
+ *   ln_w non-NULL: the LayerNorm prologue -- h = LN(x) (fp32 statistics, bf16 result, eps) is computed in the
+ *                  kernel for the call's rows and used as the GEMM input; 512 <= K <= 1024;
+ *   sw non-NULL:   w is int8 in prepare_w8's layout with per-channel scales (dec_w8_linear), else bf16 [N, K];
+ *   epilogue:      0 y = r, 1 y = ReLU(r), 2 y = bf16(y + bf16(r)) in place (the residual add; not with ln_w),
+ *                  r = x' @ w^T (scaled) + bias.
+ * M <= 64, N % 16 == 0, K % 64 == 0. */
+int cohere_dec_linear_fused(const uint16_t* x, int64_t ldx, const uint16_t* ln_w, const uint16_t* ln_b, float eps,
+                            const void* w, const float* sw, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                            int32_t epilogue, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Replaces layernorm (reference kernels/csrc/encoder_ops.cu:501-520, bound at kernels/csrc/bindings.cpp:73):
  * h = LN1(x) as bf16; with w2 (non-NULL), x = LN1(x) in place and h = LN2(x). h may be x. fp32 statistics, the
  * result rounded to bf16. cols % 8 == 0, cols <= 2048. */
