@@ -164,7 +164,7 @@ struct AttnArgs {
   const uint16_t* bv;   // (H, D)
   uint16_t* out;        // (rows, H D)
   const int32_t* tiles; // (n, 4): sequence start, sequence length, first query row, unused
-  int H, rel_off, rel_rows;
+  int H, rel_off, rel_rows, n_tiles;
   float scale;
 };
 
@@ -200,8 +200,12 @@ relpos_attention_kernel(const AttnArgs p) {
   uint16_t* sR = sVt + S::V_ELEMS;         // [128 ring slots][DP], slot = table row & 127
   uint16_t* sP = sR + S::R_ELEMS;          // [4 waves][16 queries][AT_PW]
 
-  const int4 tile = reinterpret_cast<const int4*>(p.tiles)[blockIdx.x];
-  const int start = tile.x, len = tile.y, q0 = tile.z, h = blockIdx.y;
+  // XCD-aware order: workgroup b runs on XCD b % 8, so each XCD takes a contiguous run of (head, tile) items, tiles
+  // innermost: the query tiles of one sequence and head share their keys, values and table rows in that XCD's L2
+  const int total = p.n_tiles * p.H, per = total / 8, rem = total % 8;
+  const int xcd = (int)blockIdx.x % 8, item = xcd * per + min(xcd, rem) + (int)blockIdx.x / 8;
+  const int4 tile = reinterpret_cast<const int4*>(p.tiles)[item % p.n_tiles];
+  const int start = tile.x, len = tile.y, q0 = tile.z, h = item / p.n_tiles;
   const int tid = threadIdx.x, w = wave_id(), lane = lane_id(), iq = lane & 15, g = lane >> 4;
   const int HD = p.H * D, ld = 3 * HD;
   uint16_t* sPw = sP + w * 16 * AT_PW;
@@ -408,8 +412,9 @@ extern "C" int cohere_relpos_attention(const uint16_t* qkv, const uint16_t* rk, 
   if (n_tiles == 0) return 0;
   AttnArgs p;
   p.qkv = qkv; p.rk = rk; p.bu = bu; p.bv = bv; p.out = out; p.tiles = tiles;
-  p.H = (int)heads; p.rel_off = (int)rel_off; p.rel_rows = (int)rel_rows; p.scale = scale;
-  const dim3 grid((unsigned)n_tiles, (unsigned)heads);
+  COHERE_REQUIRE(n_tiles * heads < (1LL << 31), "relpos_attention: too many tiles");
+  p.H = (int)heads; p.rel_off = (int)rel_off; p.rel_rows = (int)rel_rows; p.n_tiles = (int)n_tiles; p.scale = scale;
+  const dim3 grid((unsigned)(n_tiles * heads));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (head_dim == 160)
     relpos_attention_kernel<160><<<grid, 256, 0, s>>>(p);
