@@ -155,8 +155,9 @@ def test_encoder_layers_int8(gpu, n_layers, sparse, lengths):
     """The native layer loop against the checker's restatement of it. A whole layer re-quantizes its activations to
     int8 five times, so a last-bit difference anywhere moves whole rows by 1/127 of their maximum: the checker itself
     moves by ~0.7 % RMS per layer when 1 % of its input elements change by one bf16 ulp. The bar: the kernels' result
-    is closer to the checker than that perturbed checker is (RMS and max), and within 1e-2 x RMS for all but a few
-    percent of the elements."""
+    is closer to the checker than that perturbed checker is (RMS and max), and no more of its elements lie beyond
+    1e-2 x RMS of the checker than of the perturbed checker's. (Config 2's workload, with each launch pinned
+    separately and the drift per depth, is tests/test_encoder_config2_gpu.py.)"""
     layers = _layers(gpu, n_layers, sparse, seed=31)
     g = torch.Generator().manual_seed(32)
     x = torch.randn(sum(lengths), 1280, generator=g).to(torch.bfloat16)
@@ -174,8 +175,11 @@ def test_encoder_layers_int8(gpu, n_layers, sparse, lengths):
     print(f"layers: kernels vs checker rms {rms_gpu:.2e} max {max_gpu:.2e}; perturbed checker rms {rms_noise:.2e} "
           f"max {max_noise:.2e}")
     assert rms_gpu < rms_noise and max_gpu < max_noise
-    got_f, want_f = bf16_float(_bits(xd)), bf16_float(want)
-    assert (np.abs(got_f - want_f) > 1e-2 * np.sqrt(np.mean(want_f.astype(np.float64) ** 2))).mean() < 0.1
+    got_f, want_f, noise_f = bf16_float(_bits(xd)), bf16_float(want), bf16_float(noise)
+    bar = 1e-2 * np.sqrt(np.mean(want_f.astype(np.float64) ** 2))
+    beyond_gpu, beyond_noise = (np.abs(got_f - want_f) > bar).mean(), (np.abs(noise_f - want_f) > bar).mean()
+    print(f"beyond 1e-2 x RMS: kernels {beyond_gpu:.4f}, perturbed checker {beyond_noise:.4f}")
+    assert beyond_gpu <= beyond_noise
 
 
 def test_encoder_layers_rejects_and_noops(gpu):
