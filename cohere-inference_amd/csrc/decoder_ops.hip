@@ -27,6 +27,25 @@ constexpr int HD = 128;  // head size
 
 // ---- embedding and residual LayerNorms: one wave per row ------------------------------------------------------------
 
+// one row's embedding by one wave: x = LN0(bf16(emb[t] + ptab[p])), h = LN1(x)
+template <int VEC>
+DEVI void embed_row(int64_t t, int p, const uint16_t* emb, const uint16_t* ptab, const uint16_t* w0,
+                    const uint16_t* b0, float eps0, const uint16_t* w1, const uint16_t* b1, float eps1, uint16_t* xr,
+                    uint16_t* hr, int width, int lane) {
+  const LnParams<VEC> p0 = load_ln<VEC>(w0, b0, width, lane), p1 = load_ln<VEC>(w1, b1, width, lane);
+  Row<VEC> e, q;
+  load_row<VEC>(emb + t * width, width, lane, e);
+  load_row<VEC>(ptab + (int64_t)p * width, width, lane, q);
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) e.v[i][k] = round_bf(e.v[i][k] + q.v[i][k]);
+  ln_row<VEC>(e, width, lane, p0, eps0);
+  store_row<VEC>(e, width, lane, xr);
+  ln_row<VEC>(e, width, lane, p1, eps1);
+  store_row<VEC>(e, width, lane, hr);
+}
+
 template <int VEC>
 __global__ void __launch_bounds__(256) dec_embed_kernel(const int32_t* __restrict__ active,
                                                         const int64_t* __restrict__ tok, const int32_t* __restrict__ pos,
@@ -36,21 +55,9 @@ __global__ void __launch_bounds__(256) dec_embed_kernel(const int32_t* __restric
                                                         uint16_t* h, int rows, int width) {
   const int row = blockIdx.x * 4 + wave_id(), lane = lane_id();
   if (row >= rows) return;
-  const LnParams<VEC> p0 = load_ln<VEC>(w0, b0, width, lane), p1 = load_ln<VEC>(w1, b1, width, lane);
   const int s = active[row];
-  const int64_t t = tok[s];
-  const int p = pos[s];
-  Row<VEC> e, q;
-  load_row<VEC>(emb + t * width, width, lane, e);
-  load_row<VEC>(ptab + (int64_t)p * width, width, lane, q);
-#pragma unroll
-  for (int i = 0; i < VEC; ++i)
-#pragma unroll
-    for (int k = 0; k < 8; ++k) e.v[i][k] = round_bf(e.v[i][k] + q.v[i][k]);
-  ln_row<VEC>(e, width, lane, p0, eps0);
-  store_row<VEC>(e, width, lane, x + (int64_t)row * width);
-  ln_row<VEC>(e, width, lane, p1, eps1);
-  store_row<VEC>(e, width, lane, h + (int64_t)row * width);
+  embed_row<VEC>(tok[s], pos[s], emb, ptab, w0, b0, eps0, w1, b1, eps1, x + (int64_t)row * width,
+                 h + (int64_t)row * width, width, lane);
 }
 
 template <int VEC>
@@ -397,11 +404,22 @@ __global__ void __launch_bounds__(HD) dec_combine_kernel(const float* __restrict
 }
 
 // ---- greedy choice -------------------------------------------------------------------------------------------------
+// the next step's embedding of the row, done by the same workgroup after the choice (EVEC > 0), and the end flag
+// mirrored into host memory
+struct PickEmbed {
+  const uint16_t *emb, *ptab, *w0, *b0, *w1, *b1;
+  float eps0, eps1;
+  uint16_t *x, *h;
+  int width;
+  uint8_t* flags;  // host-mapped end flags (null: none)
+};
+
+template <int EVEC>
 __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restrict__ logits, int V,
                                                        const int32_t* __restrict__ active, int dummy, int64_t* tok,
                                                        int32_t* pos, uint8_t* finished, const int64_t* forced, int FP,
                                                        const int32_t* plen, const int32_t* limit, int64_t* out, int OUT,
-                                                       int64_t pad, int64_t eos) {
+                                                       int64_t pad, int64_t eos, const PickEmbed pe) {
   __shared__ float sb[4];
   __shared__ int sa[4];
   const int r = blockIdx.x, tid = threadIdx.x;
@@ -466,20 +484,41 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
     sa[tid >> 6] = arg;
   }
   __syncthreads();
-  if (tid != 0 || s == dummy) return;
-  for (int w = 1; w < 4; ++w)
-    if (sb[w] > best || (sb[w] == best && sa[w] < arg)) {
-      best = sb[w];
-      arg = sa[w];
+  __shared__ int64_t s_tok;
+  __shared__ int s_pos;
+  if (tid == 0) {
+    int64_t t_next = EVEC > 0 ? tok[s] : 0;
+    int p_next = EVEC > 0 ? pos[s] : 0;
+    // ended at an earlier step (or the dummy slot): nothing moves until the host retires the slot
+    if (s != dummy && !finished[s]) {
+      for (int w = 1; w < 4; ++w)
+        if (sb[w] > best || (sb[w] == best && sa[w] < arg)) {
+          best = sb[w];
+          arg = sa[w];
+        }
+      const int at = pos[s] + 1;
+      const bool in_prompt = at < plen[s];
+      const int64_t nt = in_prompt ? forced[(int64_t)s * FP + at] : (int64_t)arg;
+      const uint8_t fin = (!in_prompt && (nt == eos || at >= limit[s])) ? 1 : 0;
+      out[(int64_t)s * OUT + at] = nt;
+      tok[s] = nt;
+      pos[s] = at;
+      finished[s] = fin;
+      if (pe.flags) pe.flags[s] = fin;
+      t_next = nt;
+      p_next = at;
     }
-  if (finished[s]) return;  // ended at an earlier step: nothing moves until the host retires the slot
-  const int at = pos[s] + 1;
-  const bool in_prompt = at < plen[s];
-  const int64_t nt = in_prompt ? forced[(int64_t)s * FP + at] : (int64_t)arg;
-  out[(int64_t)s * OUT + at] = nt;
-  tok[s] = nt;
-  pos[s] = at;
-  finished[s] = (!in_prompt && (nt == eos || at >= limit[s])) ? 1 : 0;
+    if constexpr (EVEC > 0) {
+      s_tok = t_next;
+      s_pos = p_next;
+    }
+  }
+  if constexpr (EVEC > 0) {
+    __syncthreads();
+    if (tid < 64)
+      embed_row<EVEC>(s_tok, s_pos, pe.emb, pe.ptab, pe.w0, pe.b0, pe.eps0, pe.w1, pe.b1, pe.eps1,
+                      pe.x + (int64_t)r * pe.width, pe.h + (int64_t)r * pe.width, pe.width, tid);
+  }
   (void)pad;
 }
 
@@ -644,9 +683,49 @@ extern "C" int cohere_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, 
   COHERE_REQUIRE(logits && active && tok && pos && finished && forced && plen && limit && out && al16(logits),
                  "dec_pick: bad pointer");
   if (rows == 0) return 0;
-  dec_pick_kernel<<<(unsigned)rows, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
-      logits, (int)V, active, (int)dummy, tok, pos, finished, forced, (int)FP, plen, limit, out, (int)OUT, pad, eos);
+  dec_pick_kernel<0><<<(unsigned)rows, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      logits, (int)V, active, (int)dummy, tok, pos, finished, forced, (int)FP, plen, limit, out, (int)OUT, pad, eos,
+      PickEmbed{});
   return cohere::check_launch("dec_pick");
+}
+
+extern "C" int cohere_dec_pick_embed(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active,
+                                     int64_t dummy, int64_t* tok, int32_t* pos, uint8_t* finished,
+                                     const int64_t* forced, int64_t FP, const int32_t* plen, const int32_t* limit,
+                                     int64_t* out, int64_t OUT, int64_t pad, int64_t eos, const uint16_t* emb,
+                                     const uint16_t* ptab, const uint16_t* w0, const uint16_t* b0, float eps0,
+                                     const uint16_t* w1, const uint16_t* b1, float eps1, uint16_t* x, uint16_t* h,
+                                     int64_t width, uint8_t* flags_host, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(rows >= 0 && V > 0 && V % 8 == 0, "dec_pick_embed: the vocabulary must be a multiple of 8");
+  COHERE_REQUIRE(logits && active && tok && pos && finished && forced && plen && limit && out && al16(logits),
+                 "dec_pick_embed: bad pointer");
+  COHERE_REQUIRE(width > 0 && width % 8 == 0 && width <= 2048,
+                 "dec_pick_embed: width must be a multiple of 8, at most 2048");
+  COHERE_REQUIRE(emb && ptab && w0 && b0 && w1 && b1 && x && h && al16(emb) && al16(ptab) && al16(x) && al16(h) &&
+                     al16(w0) && al16(b0) && al16(w1) && al16(b1),
+                 "dec_pick_embed: bad embedding pointer");
+  uint8_t* flags_dev = nullptr;
+  if (flags_host) {
+    void* d = nullptr;
+    COHERE_REQUIRE(hipHostGetDevicePointer(&d, flags_host, 0) == hipSuccess && d,
+                   "dec_pick_embed: the end flags must be pinned host memory");
+    flags_dev = static_cast<uint8_t*>(d);
+  }
+  if (rows == 0) return 0;
+  const PickEmbed pe{emb, ptab, w0, b0, w1, b1, eps0, eps1, x, h, (int)width, flags_dev};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+#define PICK(VV)                                                                                                   \
+  dec_pick_kernel<VV><<<(unsigned)rows, 256, 0, st>>>(logits, (int)V, active, (int)dummy, tok, pos, finished, forced, \
+                                                      (int)FP, plen, limit, out, (int)OUT, pad, eos, pe)
+  switch (vec_of(width)) {
+    case 1: PICK(1); break;
+    case 2: PICK(2); break;
+    case 3: PICK(3); break;
+    default: PICK(4); break;
+  }
+#undef PICK
+  return cohere::check_launch("dec_pick_embed");
 }
 
 namespace {

@@ -36,7 +36,7 @@ EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_l
            "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
            "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8", "cohere_gemm_bf16", "cohere_logmel_workspace_bytes",
            "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw", "cohere_encoder_branch_workspace_bytes",
-           "cohere_encoder_layers_noalloc", "cohere_dec_linear_fused")
+           "cohere_encoder_layers_noalloc", "cohere_dec_linear_fused", "cohere_dec_pick_embed")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -64,6 +64,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_dec_attention": [I32, P, I64, P, I64, P, P, P, I64, I64, F, I64, P, I64, P, P],
         "cohere_dec_attention_q8": [I32, P, I64, P, I64, P, P, P, P, P, I64, I64, F, I64, P, I64, P, P],
         "cohere_dec_pick": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P],
+        "cohere_dec_pick_embed": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P, P, P, P, F, P, P, F,
+                                  P, P, I64, P, P],
         "cohere_dec_scatter_kv": [P, I64, P, P, P, P, I64, I64, I64, I64, P],
         "cohere_dec_scatter_kv_q8": [P, I64, P, P, P, P, P, P, I64, I64, I64, I64, P],
         "cohere_gemm_bf16": [P, I64, P, P, P, I64, I32, P, I64, F, I64, I64, I64, I32, P],
@@ -468,6 +470,26 @@ class _Ext:
         self._call("cohere_dec_pick", _ptr(logits), rows, V, _ptr(active), int(dummy), _ptr(tok), _ptr(pos),
                    _ptr(finished), _ptr(forced), forced.shape[1], _ptr(plen), _ptr(limit), _ptr(out), out.shape[1],
                    int(pad), int(eos), _stream())
+
+    def dec_pick_embed(self, logits, active, dummy, tok, pos, finished, forced, plen, limit, out, pad, eos, emb, ptab,
+                       w0, b0, eps0, w1, b1, eps1, x, h, flags=None):
+        """dec_pick, then each row's next embedding as dec_embed computes it (x, h), and, with flags (pinned uint8 per
+        slot on the host), the stepped slots' end flags written there (no single counterpart in the reference: its
+        step ends with dec_pick and a copy of the flags, and the next one starts with dec_embed)."""
+        _check(logits.is_contiguous() and logits.shape[1] % 8 == 0, "dec_pick_embed: contiguous logits, V % 8 == 0")
+        _check(tok.dtype == torch.int64 and forced.dtype == torch.int64 and out.dtype == torch.int64 and
+               finished.dtype == torch.uint8, "dec_pick_embed: dtypes")
+        _check(x.is_contiguous() and h.is_contiguous() and x.dtype == h.dtype == emb.dtype == torch.bfloat16 and
+               x.shape[0] == logits.shape[0], "dec_pick_embed: contiguous bf16 x, h, a row per logits row")
+        _check(flags is None or (flags.device.type == "cpu" and flags.is_pinned() and flags.dtype == torch.uint8 and
+                                 flags.numel() >= finished.numel()), "dec_pick_embed: flags pinned uint8, one per slot")
+        rows, V = logits.shape
+        width = x.shape[1]
+        _check(emb.shape[1] == width and ptab.shape[1] == width, "dec_pick_embed: widths")
+        self._call("cohere_dec_pick_embed", _ptr(logits), rows, V, _ptr(active), int(dummy), _ptr(tok), _ptr(pos),
+                   _ptr(finished), _ptr(forced), forced.shape[1], _ptr(plen), _ptr(limit), _ptr(out), out.shape[1],
+                   int(pad), int(eos), _ptr(emb), _ptr(ptab), _ptr(w0), _ptr(b0), float(eps0), _ptr(w1), _ptr(b1),
+                   float(eps1), _ptr(x), _ptr(h), width, _ptr(flags), _stream())
 
     def dec_scatter_kv(self, kv, slot_of, frame_of, ck, cv):
         """Cross-attention keys/values of packed frames into their slots (decoder_ops.cu:316-327)."""

@@ -230,6 +230,7 @@ class StreamDecoder:
                                 dtype=torch.float32)
 
         self.stream = torch.cuda.Stream(device=dev)
+        self._embed_stale, self._embed_rows = True, 0
         self.programs = {b: self._program(b) for b in self.buckets}
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         if capture:
@@ -264,11 +265,12 @@ class StreamDecoder:
         act, x, hn, att = self.active[:b], self.x[:b], self.hn[:b], self.att[:b]
         qkv, q, proj, ffn, logits = (t[:b] for t in (self.qkv_out, self.q_out, self.proj_out, self.ffn_out,
                                                      self.logits))
-        ops = [lambda: ext.dec_embed(act, self.tok, self.pos, self.embed, self.pos_table, *self.emb_ln,
-                                     *self.blocks[0].norms[0], x, hn)]
         if self.fused:
             # the residual adds ride on o / cross-o / fc2's epilogues and the LayerNorms on the next projection's
-            # prologue: 8 launches a layer instead of 11, the same bits
+            # prologue (8 launches a layer instead of 11); the pick computes the next step's embedding of its row and
+            # writes the end flags to the host itself. The same bits as the unfused step. The step's own embedding
+            # comes from the previous step's pick, or from step() when the rows changed.
+            ops = []
             for i, blk in enumerate(self.blocks):
                 first = i == 0
                 ops += [(lambda blk=blk: blk.qkv.fused(hn, qkv)) if first else
@@ -281,10 +283,12 @@ class StreamDecoder:
                         lambda blk=blk: blk.fc1.fused(x, ffn, DEC_EP_RELU, ln=blk.norms[2]),
                         lambda blk=blk: blk.fc2.fused(ffn, x, DEC_EP_RESID)]
             ops += [lambda: self.head.fused(x, logits, ln=self.final_ln),
-                    lambda: ext.dec_pick(logits, act, self.dummy, self.tok, self.pos, self.finished, self.forced,
-                                         self.plen, self.limit, self.out, self.pad, self.eos),
-                    lambda: self.flags.copy_(self.finished, non_blocking=True)]
+                    lambda: ext.dec_pick_embed(logits, act, self.dummy, self.tok, self.pos, self.finished, self.forced,
+                                               self.plen, self.limit, self.out, self.pad, self.eos, self.embed,
+                                               self.pos_table, *self.emb_ln, *self.blocks[0].norms[0], x, hn,
+                                               self.flags)]
             return ops
+        ops = [lambda: self._embed(b)]
         for i, blk in enumerate(self.blocks):
             after_ffn = self.blocks[i + 1].norms[0] if i + 1 < len(self.blocks) else self.final_ln
             ops += [lambda blk=blk: blk.qkv(hn, qkv),
@@ -304,7 +308,14 @@ class StreamDecoder:
                 lambda: self.flags.copy_(self.finished, non_blocking=True)]
         return ops
 
+    def _embed(self, b: int) -> None:
+        """The embedding and first LayerNorm of the first b active rows (x, hn), on the current stream."""
+        ext.dec_embed(self.active[:b], self.tok, self.pos, self.embed, self.pos_table, *self.emb_ln,
+                      *self.blocks[0].norms[0], self.x[:b], self.hn[:b])
+
     def _run(self, b: int) -> None:
+        if self.fused:
+            self._embed(b)
         for op in self.programs[b]:
             op()
 
@@ -318,7 +329,8 @@ class StreamDecoder:
                 self.stream.synchronize()
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g, stream=self.stream):
-                    self._run(b)
+                    for op in self.programs[b]:  # the program only: step() adds the embedding when the rows change
+                        op()
                 self.graphs[b] = g
         self.reset()
         self.stream.synchronize()
@@ -327,6 +339,7 @@ class StreamDecoder:
 
     def reset(self) -> None:
         """Every slot free (on the decoder stream)."""
+        self._embed_stale = True
         with torch.cuda.stream(self.stream):
             self.finished.fill_(1)
             self.pos.zero_()
@@ -400,6 +413,7 @@ class StreamDecoder:
             self.cross_len.index_copy_(0, idx, nums_d[:, 2].contiguous())
             self.finished.index_fill_(0, idx, 0)
         self.flags[torch.tensor(slots, dtype=torch.long)] = 0
+        self._embed_stale = True
 
     def set_active(self, slots: list[int]) -> int:
         """The active rows of the next steps (on the decoder stream), padded with the dummy slot; returns the
@@ -409,15 +423,21 @@ class StreamDecoder:
         host[:len(slots)] = torch.tensor(slots, dtype=torch.int32)
         with torch.cuda.stream(self.stream):
             self.active[:b].copy_(self._to_device(host))
+        self._embed_stale = True
         return b
 
     def step(self, bucket: int) -> None:
-        """One decoding step of the first `bucket` active rows (a graph replay on the decoder stream)."""
+        """One decoding step of the first `bucket` active rows (a graph replay on the decoder stream). With the fused
+        program the rows' embeddings come from the previous step's pick; after admit / set_active / reset, or on a
+        different bucket, they are computed first."""
         with torch.cuda.stream(self.stream):
             if bucket in self.graphs:
+                if self.fused and (self._embed_stale or bucket != self._embed_rows):
+                    self._embed(bucket)
                 self.graphs[bucket].replay()
             else:
                 self._run(bucket)
+            self._embed_stale, self._embed_rows = False, bucket
 
     def weight_bytes(self) -> int:
         """Bytes of projection weights one step reads."""

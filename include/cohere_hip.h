@@ -197,6 +197,19 @@ int cohere_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, const int32
                     const int32_t* plen, const int32_t* limit, int64_t* out, int64_t OUT, int64_t pad, int64_t eos,
                     void* stream);
 
+/* No single counterpart in the reference: its step ends with dec_pick (kernels/csrc/decoder_ops.cu:106-159) and the
+ * end flags' copy to the host, and the next step starts with dec_embed (decoder_ops.cu:24-54; stream_decoder.py:
+ * 176-199). This entry point is dec_pick, then, by the same workgroup, the row's next embedding exactly as dec_embed
+ * computes it from the slot's (possibly new) token and position -- x / h [rows, width] -- and, with flags_host
+ * non-NULL (pinned host memory, one byte per slot), each stepped slot's end flag written there. Arguments as
+ * cohere_dec_pick followed by cohere_dec_embed's tables and LayerNorms. */
+int cohere_dec_pick_embed(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active, int64_t dummy,
+                          int64_t* tok, int32_t* pos, uint8_t* finished, const int64_t* forced, int64_t FP,
+                          const int32_t* plen, const int32_t* limit, int64_t* out, int64_t OUT, int64_t pad,
+                          int64_t eos, const uint16_t* emb, const uint16_t* ptab, const uint16_t* w0,
+                          const uint16_t* b0, float eps0, const uint16_t* w1, const uint16_t* b1, float eps1,
+                          uint16_t* x, uint16_t* h, int64_t width, uint8_t* flags_host, void* stream);
+
 /* Replaces dec_scatter_kv (reference kernels/csrc/decoder_ops.cu:163-175, 316-327, bound at
  * kernels/csrc/bindings.cpp:84): kv bf16 [rows, L x 2 x H x 128] (per layer: keys of every head, then values) of
  * packed encoder frames, row i = frame frame_of[i] of slot slot_of[i], into caches ck, cv (L, S, H, T, 128). */

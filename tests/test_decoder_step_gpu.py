@@ -294,3 +294,6 @@ def test_fused_step_matches_unfused(int8, gpu):
         assert torch.equal(a.logits[:bs[0]].view(torch.int16), b.logits[:bs[0]].view(torch.int16))
         for name in ("tok", "pos", "out", "finished", "self_k", "self_v"):
             assert torch.equal(getattr(a, name), getattr(b, name)), name
+        # the fused pick writes the stepped slots' end flags to the host itself; the unfused step copies them
+        assert np.array_equal(a.flags.numpy()[slots], b.flags.numpy()[slots])
+        assert np.array_equal(a.flags.numpy()[slots], a.finished.cpu().numpy()[slots])
