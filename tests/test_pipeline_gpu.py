@@ -140,3 +140,48 @@ def test_submit_matches_transcribe(gpu):
         assert np.array_equal(a, b) and len(a) <= len(prompt) + n
     with pytest.raises(RuntimeError, match="transcribe"):
         pipe.transcribe(xs, prompt)
+
+
+def test_submit_from_threads_and_failed_chunk(gpu):
+    """Requests submitted from four threads at once each get the tokens transcribe() gives for their pieces; a chunk
+    whose encoding raises fails exactly the requests it held (their futures raise), and the service goes on."""
+    import threading
+
+    import bench
+    from kernels.pipeline import Pipeline
+
+    model = bench.random_asr_model(gpu, enc_layers=1, seed=7)
+    pipe = Pipeline(model, None, 4, 8, True, True, buckets=(1, 2, 4))
+    lengths = [[32000], [17600, 9600], [52800], [24000]]
+    audio = [[Pipeline.prepare(x) for x in bench.synthetic_audio(ls, seed=20 + i)] for i, ls in enumerate(lengths)]
+    prompt = torch.tensor([4, 5, 6, 7])
+    want = [pipe.transcribe([torch.from_numpy(x).to(gpu) for x in xs], prompt) for xs in audio]
+    futures = [None] * len(audio)
+
+    def client(i):
+        futures[i] = pipe.submit(audio[i], prompt)
+
+    threads = [threading.Thread(target=client, args=(i,)) for i in range(len(audio))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    for f, w in zip(futures, want):
+        got = f.result(timeout=120)
+        assert len(got) == len(w) and all(np.array_equal(a, b) for a, b in zip(got, w))
+
+    # a chunk whose encoding fails: its request fails, the next request is served
+    real = pipe._encode
+
+    def flaky(pieces, slots):
+        if any(p.n == 11200 for p in pieces):
+            raise RuntimeError("injected encoder failure")
+        return real(pieces, slots)
+
+    pipe._encode = flaky
+    bad = pipe.submit([Pipeline.prepare(x) for x in bench.synthetic_audio([11200], seed=30)], prompt)
+    with pytest.raises(RuntimeError, match="injected"):
+        bad.result(timeout=120)
+    good = pipe.submit(audio[0], prompt).result(timeout=120)
+    assert np.array_equal(good[0], want[0][0])
+    pipe.close()
