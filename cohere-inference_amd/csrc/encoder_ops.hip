@@ -148,8 +148,9 @@ constexpr int AT_Q = 64, AT_KEYS = 32, AT_RING = 128, AT_PW = 52;  // per-wave p
 
 template <int D>
 struct AttnShape {
-  static constexpr int DP = D + 8;            // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
   static constexpr int KS = (D + 31) / 32;    // k steps of 32 over the head size (the last one zero-padded)
+  static constexpr int DK = KS * 32;          // the head size padded to whole k steps; columns D .. DK stay zero
+  static constexpr int DP = DK + 8;           // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
   static constexpr int OB = D / 16;           // 16-dim blocks of the output
   static constexpr int VT = AT_KEYS + 4;      // LDS row of the transposed value tile
   static constexpr int K_ELEMS = AT_KEYS * DP, V_ELEMS = D * VT, R_ELEMS = AT_RING * DP, P_ELEMS = 4 * 16 * AT_PW;
@@ -168,10 +169,9 @@ struct AttnArgs {
   float scale;
 };
 
-// 8 bf16 of an LDS row as an MFMA operand; zero past the head size (the padded last k step)
+// 8 bf16 of an LDS row as an MFMA operand (past the head size the row's padding columns, kept zero)
 template <int D>
 DEVI v8bf lds_op(const uint16_t* row, int col) {
-  if (D % 32 != 0 && col >= D) return v8bf{};
   return *reinterpret_cast<const v8bf*>(row + col);
 }
 
@@ -221,6 +221,17 @@ relpos_attention_kernel(const AttnArgs p) {
     qvb[ks] = q_plus<D>(qptr, p.bv + h * D, ks * 32 + g * 8, qvalid);
   }
 
+  // the K and table rows' columns D .. DK: zero for good (the tiles write columns below D only); published by the
+  // first tile's barrier
+  if constexpr (S::DK > D) {
+    constexpr int PADC = (S::DK - D) / 8;  // 16-byte chunks of padding per row
+    for (int id = tid; id < (AT_KEYS + AT_RING) * PADC; id += 256) {
+      const int row = id / PADC, c = D + (id % PADC) * 8;
+      uint16_t* dst = row < AT_KEYS ? sK + row * S::DP + c : sR + (row - AT_KEYS) * S::DP + c;
+      *reinterpret_cast<uint4*>(dst) = make_uint4(0, 0, 0, 0);
+    }
+  }
+
   v4f o[S::OB];
 #pragma unroll
   for (int i = 0; i < S::OB; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -228,25 +239,29 @@ relpos_attention_kernel(const AttnArgs p) {
 
   const uint16_t* kbase = p.qkv + (int64_t)start * ld + HD + h * D;
   const uint16_t* vbase = kbase + HD;
+  const uint16_t* rbase = p.rk + h * D;
   constexpr int CH = D / 8;  // 16-byte chunks per row
-  // a key tile's global data: keys j0 .. j0 + 31 (zero past the sequence), their values, and the 32 table rows of
+  // a key tile's global data: keys j0 .. j0 + 31 (clamped to the sequence), their values, and the 32 table rows of
   // distances q0 - j0 - 31 .. q0 - j0 (the tile reads distances up to q0 - j0 + 63; the previous tiles brought
   // those). Loaded into registers one tile ahead, so the loads of tile j0 + 32 fly while tile j0 computes.
   constexpr int NC = (AT_KEYS * CH + 255) / 256;  // 16-byte chunks per thread and array
   uint4 pk[NC], pv[NC], pr[NC];
+#pragma unroll
+  for (int x = 0; x < NC; ++x) pk[x] = pv[x] = pr[x] = make_uint4(0, 0, 0, 0);  // once: the chunks past 32 rows
   auto fetch = [&](int j0) {
 #pragma unroll
     for (int x = 0; x < NC; ++x) {
       const int id = tid + x * 256;
-      pk[x] = pv[x] = pr[x] = make_uint4(0, 0, 0, 0);
       if (id < AT_KEYS * CH) {
-        const int r = id / CH, c = (id % CH) * 8, key = j0 + r;
-        if (key < len) {
-          pk[x] = *reinterpret_cast<const uint4*>(kbase + (int64_t)key * ld + c);
-          pv[x] = *reinterpret_cast<const uint4*>(vbase + (int64_t)key * ld + c);
-        }
+        // 32-bit element offsets from uniform bases (a layer's qkv and table stay below 2^31 elements). Keys past
+        // the sequence load its last key: their scores are masked and their probabilities exactly 0 (the values
+        // finite), so no register is zeroed
+        const int r = id / CH, c = (id % CH) * 8, key = min(j0 + r, len - 1);
+        const uint32_t off = (uint32_t)key * (uint32_t)ld + (uint32_t)c;
+        pk[x] = *reinterpret_cast<const uint4*>(kbase + off);
+        pv[x] = *reinterpret_cast<const uint4*>(vbase + off);
         const int d = q0 - j0 - (AT_KEYS - 1) + r, trow = min(max(d + p.rel_off, 0), p.rel_rows - 1);
-        pr[x] = *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
+        pr[x] = *reinterpret_cast<const uint4*>(rbase + ((uint32_t)trow * (uint32_t)HD + (uint32_t)c));
       }
     }
   };
