@@ -347,9 +347,13 @@ relpos_attention_kernel(const AttnArgs p) {
     }
     rs = xor32_sum(xor16_sum(rs));
     l = l * alpha + rs;
+    // the rescale only when some query of the wave has a new maximum (alpha == 1 elsewhere: o * 1 is o, bit for bit)
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int ob = 0; ob < S::OB; ++ob) o[ob] *= alpha;
+    }
 #pragma unroll
     for (int ob = 0; ob < S::OB; ++ob) {
-      o[ob] *= alpha;
       const uint16_t* vrow = sVt + (ob * 16 + iq) * S::VT;
       const uint2 lo = *reinterpret_cast<const uint2*>(vrow + g * 4);
       const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 + g * 4);
