@@ -294,12 +294,10 @@ dec_attention_kernel(const DecAttnArgs p) {
   int j0 = start + grp;
   // a pass's loads are issued at the top of the pass: no registers carry loaded keys across passes, so one pass of KB
   // keys per group fits the register budget. Caches of more than KB * AG = 512 keys pay one more memory round trip
-  // per pass.
-  for (bool first = true; j0 < end; j0 += KB * AG, first = false) {
-    if (!(first && early)) {
-      if (LDSV && !first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
-      load_pass(j0, end);
-    }
+  // per pass. One pass over the loaded keys is a lambda, so that the early pass runs outside the loop (a loop whose
+  // first pass could come from registers loaded before it made the compiler copy every loaded register at its back
+  // edge).
+  auto process = [&](int j0) {
     float sc[KB], mb = m;
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
@@ -333,6 +331,15 @@ dec_attention_kernel(const DecAttnArgs p) {
       __builtin_amdgcn_sched_barrier(0);
     }
     m = mb;
+  };
+  if (early) {
+    if (j0 < end) process(j0);
+    j0 += KB * AG;
+  }
+  for (bool first = true; j0 < end; j0 += KB * AG, first = false) {
+    if (LDSV && !first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
+    load_pass(j0, end);
+    process(j0);
   }
   // LDSV: every wave is done reading its values (and an early pass has landed) before the buffer holds the partial
   // outputs
