@@ -19,6 +19,10 @@
 //    agent-scope release/acquire that writes back and invalidates L2 -- far costlier than these GEMMs. The result is
 //    deterministic and the kernel is graph-replayable with no state; the reference's workspace and counters are
 //    accepted (and checked as it checks them) but not needed.
+//  * Fused forms for the decoder step (cohere_dec_linear_fused): a LayerNorm prologue (each wave normalises rows of
+//    the workgroup's block with dec_add_ln's arithmetic into LDS, and the K loop reads the activations there) and a
+//    residual epilogue (y = bf16(y + bf16(result)), dec_add_ln's sum, in place). Folding the step's residual
+//    LayerNorms into the projections this way gives the same bits as the separate launches.
 #include "common.h"
 #include "cohere_hip.h"
 #include "rows.h"
