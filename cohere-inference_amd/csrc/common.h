@@ -55,6 +55,27 @@ DEVI float dpp_mov(float v) {
 }
 DEVI float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
 
+// lane I of each aligned group of 8 lanes, in every lane of the group: a quad broadcast of lane I % 4, then the
+// group's other quad takes it across the half mirror (bank mask: only that quad's lanes are written)
+template <int I>
+DEVI float group8_bcast_c(float v) {
+  constexpr int k = I & 3;
+  const int x = __builtin_amdgcn_update_dpp(0, __float_as_int(v), k | k << 2 | k << 4 | k << 6, 0xF, 0xF, false);
+  return __int_as_float(__builtin_amdgcn_update_dpp(x, x, DPP_HALF_MIRROR, 0xF, I < 4 ? 0xA : 0x5, false));
+}
+// the same for an index that is a constant after unrolling
+DEVI float group8_bcast(float v, int i) {
+  switch (i) {
+    case 0: return group8_bcast_c<0>(v);
+    case 1: return group8_bcast_c<1>(v);
+    case 2: return group8_bcast_c<2>(v);
+    case 3: return group8_bcast_c<3>(v);
+    case 4: return group8_bcast_c<4>(v);
+    case 5: return group8_bcast_c<5>(v);
+    case 6: return group8_bcast_c<6>(v);
+    default: return group8_bcast_c<7>(v);
+  }
+}
 // over each aligned group of 8 lanes, in every lane of the group
 DEVI float group8_sum(float v) {
   v += dpp_mov<DPP_XOR1>(v);
@@ -116,6 +137,27 @@ DEVI float wave_max_xor(float v, int width) {
 
 // wait for this wave's outstanding vector-memory operations (incl. global -> LDS transfers)
 DEVI void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// wait until at most n (0..15, a constant after unrolling) of the wave's vector memory operations are in flight
+DEVI void wait_vm_upto(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+  }
+}
 
 // workgroup barrier for LDS pipelines: this wave's LDS operations complete, then s_barrier. Unlike __syncthreads()
 // it carries no memory fence, so the compiler does not drain the global -> LDS transfers still in flight for later

@@ -201,17 +201,40 @@ dec_attention_kernel(const DecAttnArgs p) {
   auto vblock = [&](int i, int c) { return sbuf + ((i * VB + c) * 8 + wave) * 1024; };
   uint4 kr[KB][Q8 ? 1 : 2], vr[LDSV ? 1 : KB][Q8 ? 1 : 2];
   // int8 scales: lane gl of a group loads the scales of the group's key gl of the pass (one load each for the key
-  // and value scales, where one load per key made 16 narrow loads per lane), handed to the group's lanes by index
+  // and value scales, where one load per key made 16 narrow loads per lane): the lane that ends up with that key's
+  // dot product
   float ksl = 1.f, vsl = 1.f;
-  auto group_lane = [&](float v, int i) {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(((tid & 56) | i) << 2, __float_as_int(v)));
-  };
   // 32-bit offsets from the layer's cache base (a layer's cache stays below 2^32 elements), so that the loads take
   // the uniform base in scalar registers and one offset register each
   const uint32_t vrow0 = (uint32_t)vec0;
+  // key slot i of a pass is live for the wave while its first group's key j0w + i * AG is below the limit (the
+  // wave's groups are consecutive, so the others' keys of that slot are past it too): slots past the end for the
+  // whole wave are neither loaded nor computed (a scalar branch; short caches do a fraction of a pass)
+  auto wave_first = [&](int j0) { return __builtin_amdgcn_readfirstlane(j0 - (grp & 7)); };
+  // issue order: the scales, the keys, then the values
   auto load_pass = [&](int j0, int limit) {
+    const int j0w = wave_first(j0);
+    if constexpr (Q8) {  // byte offsets in 32 bits: the loads then use the scalar base (one offset register each)
+      const int jj = j0 + gl * AG;
+      const uint32_t off = (vrow0 + (uint32_t)(jj < limit ? jj : 0)) << 2;
+      ksl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.ks) + off);
+      vsl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.vs) + off);
+    }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
+      if (j0w + i * AG >= limit) break;
+      const int jj = j0 + i * AG;
+      const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
+      if constexpr (Q8) {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + (vec * HD + gl * 16));
+      } else {
+        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16));
+        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16 + 8));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      if (j0w + i * AG >= limit) break;
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (!LDSV) {
@@ -227,23 +250,6 @@ dec_attention_kernel(const DecAttnArgs p) {
         const uint16_t* src = p.v + (vec * HD + gl * 16);
         __builtin_amdgcn_global_load_lds(src, (LDS_AS void*)vblock(i, 0), 16, 0, 0);
         __builtin_amdgcn_global_load_lds(src + 8, (LDS_AS void*)vblock(i, 1), 16, 0, 0);
-      }
-    }
-    if constexpr (Q8) {  // byte offsets in 32 bits: the loads then use the scalar base (one offset register each)
-      const int jj = j0 + gl * AG;
-      const uint32_t off = (vrow0 + (uint32_t)(jj < limit ? jj : 0)) << 2;
-      ksl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.ks) + off);
-      vsl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.vs) + off);
-    }
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      const int jj = j0 + i * AG;
-      const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
-      if constexpr (Q8) {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k8 + (vec * HD + gl * 16));
-      } else {
-        kr[i][0] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16));
-        kr[i][1] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16 + 8));
       }
     }
   };
@@ -269,11 +275,22 @@ dec_attention_kernel(const DecAttnArgs p) {
   float m = -INFINITY, l = 0.f, acc[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) acc[k] = 0.f;
-  if (SELF && sp == 0 && grp == 0) {  // the new key and value: into the cache at n, and attended as computed
+  // self-attention: the new key and value go into the cache at n and are attended as computed. Their loads are issued
+  // here and the work is done after the first pass's cache loads are issued (the cache's keys below n are not
+  // touched by it), so the workgroup's first wave does not pay a memory round trip of its own before its pass.
+  const bool fresh = SELF && sp == 0 && grp == 0;
+  uint4 knr[2], vnr[2];
+  const uint16_t* nrow = p.q + (int64_t)r * p.ldq + p.H * HD + h * HD + gl * 16;
+  if (fresh) {
+    knr[0] = *reinterpret_cast<const uint4*>(nrow);
+    knr[1] = *reinterpret_cast<const uint4*>(nrow + 8);
+    vnr[0] = *reinterpret_cast<const uint4*>(nrow + p.H * HD);
+    vnr[1] = *reinterpret_cast<const uint4*>(nrow + p.H * HD + 8);
+  }
+  auto new_token = [&]() {
     float kn[16], vn[16];
-    const uint16_t* row = p.q + (int64_t)r * p.ldq + p.H * HD + h * HD + gl * 16;
-    load16_bf(row, kn);
-    load16_bf(row + p.H * HD, vn);
+    unpack_bf(knr[0], knr[1], kn);
+    unpack_bf(vnr[0], vnr[1], vn);
     const int64_t vec = vec0 + n;
     if constexpr (Q8) {
       store16_q8(kn, p.k8 + vec * HD + gl * 16, p.ks + vec, gl);
@@ -281,13 +298,13 @@ dec_attention_kernel(const DecAttnArgs p) {
     } else {
       uint16_t* kd = p.k + vec * HD + gl * 16;
       uint16_t* vd = p.v + vec * HD + gl * 16;
-      *reinterpret_cast<uint4*>(kd) = *reinterpret_cast<const uint4*>(row);
-      *reinterpret_cast<uint4*>(kd + 8) = *reinterpret_cast<const uint4*>(row + 8);
-      *reinterpret_cast<uint4*>(vd) = *reinterpret_cast<const uint4*>(row + p.H * HD);
-      *reinterpret_cast<uint4*>(vd + 8) = *reinterpret_cast<const uint4*>(row + p.H * HD + 8);
+      *reinterpret_cast<uint4*>(kd) = knr[0];
+      *reinterpret_cast<uint4*>(kd + 8) = knr[1];
+      *reinterpret_cast<uint4*>(vd) = vnr[0];
+      *reinterpret_cast<uint4*>(vd + 8) = vnr[1];
     }
     attend_one(q, kn, vn, p.scale, m, l, acc);
-  }
+  };
   const int chunk = (n + nsp - 1) / nsp, start = sp * chunk, end = min(n, start + chunk);
   // each group takes KB keys per pass (every 64th key), all loads issued before any use: one memory round trip per
   // pass; then one softmax update for the pass
@@ -297,52 +314,86 @@ dec_attention_kernel(const DecAttnArgs p) {
   // per pass. One pass over the loaded keys is a lambda, so that the early pass runs outside the loop (a loop whose
   // first pass could come from registers loaded before it made the compiler copy every loaded register at its back
   // edge).
+  // One pass over the loaded keys. Each lane holds its 16 dimensions' partial dot product with every key of the pass;
+  // a transposed reduction over the group's 8 lanes (exchange half the keys with the lane 4 away, then 2, then 1)
+  // leaves lane gl with the whole dot product of key kx = gl (KB 8) or gl / 2 (KB 4) in 7 (3) lane moves -- the lane
+  // that also holds that key's int8 scale. The pass's maximum and sum of weights go over the group's lanes; the
+  // weights reach the value loop by a broadcast from the key's lane.
+  const int kx = KB == 8 ? gl : gl >> 1;
   auto process = [&](int j0) {
-    float sc[KB], mb = m;
+    const int j0w = wave_first(j0);
+    float d[KB];
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
+      d[i] = 0.f;
+      if (j0w + i * AG >= end) continue;
       float kk[16];
       if constexpr (Q8) unpack_q8(kr[i][0], 1.f, kk);  // the integers; the key's scale multiplies the dot product
       else unpack_bf(kr[i][0], kr[i][1], kk);
-      float d = 0.f;
+      float t = 0.f;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) d = __builtin_fmaf(q[k], kk[k], d);
-      d = group_sum(d);
-      if constexpr (Q8) d *= group_lane(ksl, i);
-      sc[i] = j0 + i * AG < end ? d * p.scale : -INFINITY;
-      mb = fmaxf(mb, sc[i]);
-      __builtin_amdgcn_sched_barrier(0);  // one key's unpacked values at a time (register pressure)
+      for (int k = 0; k < 16; ++k) t = __builtin_fmaf(q[k], kk[k], t);
+      d[i] = t;
     }
-    const float a = __expf(m - mb);
-    l *= a;
+    // lanes 0-3 of the group keep the first half of the keys, lanes 4-7 the second: send the other half across the
+    // half mirror (lane i <-> 7 - i) and add what comes back; then the same within each half across lane ^ 2 and ^ 1
+    const bool hi4 = gl & 4, hi2 = gl & 2, hi1 = gl & 1;
+    float d1[KB / 2];
+#pragma unroll
+    for (int j = 0; j < KB / 2; ++j) {
+      const float keep = hi4 ? d[j + KB / 2] : d[j], give = hi4 ? d[j] : d[j + KB / 2];
+      d1[j] = keep + dpp_mov<DPP_HALF_MIRROR>(give);
+    }
+    float d2[KB / 4];
+#pragma unroll
+    for (int j = 0; j < KB / 4; ++j) {
+      const float keep = hi2 ? d1[j + KB / 4] : d1[j], give = hi2 ? d1[j] : d1[j + KB / 4];
+      d2[j] = keep + dpp_mov<DPP_XOR2>(give);
+    }
+    float dk;
+    if constexpr (KB == 8) {
+      const float keep = hi1 ? d2[1] : d2[0], give = hi1 ? d2[0] : d2[1];
+      dk = keep + dpp_mov<DPP_XOR1>(give);
+    } else {
+      dk = d2[0] + dpp_mov<DPP_XOR1>(d2[0]);  // both lanes of a pair hold the key's sum
+    }
+    if constexpr (Q8) dk *= ksl;
+    const float sc = j0 + kx * AG < end ? dk * p.scale : -INFINITY;
+    const float mb = fmaxf(m, group_max(sc));
+    const float a = __expf(m - mb), e = __expf(sc - mb);
+    l = __builtin_fmaf(l, a, group_sum(KB == 8 || !hi1 ? e : 0.f));
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] *= a;
-    // LDSV: the pass's values have landed in LDS once every load of the wave is done (the copies were issued first)
-    if constexpr (LDSV) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const float ew = Q8 ? e * vsl : e;  // int8: the value's scale goes into the weight
+    // LDSV with every slot live: value i has landed in LDS once at most the younger copies are still in flight
+    // (stores issued later only make the wait longer); with fewer live slots, all of them
+    const bool full = j0w + (KB - 1) * AG < end;
+    if (LDSV && !full) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
-      const float e = __expf(sc[i] - mb);
-      l += e;
+      if (j0w + i * AG >= end) break;
+      if (LDSV && full) wait_vm_upto((KB - 1 - i) * VB);
+      const float w = group8_bcast(ew, KB == 8 ? i : 2 * i);
       float vv[16];
-      read_v(i, vv);  // int8: the integers; the value's scale goes into the weight
-      const float ew = Q8 ? e * group_lane(vsl, i) : e;
+      read_v(i, vv);
 #pragma unroll
-      for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(ew, vv[k], acc[k]);
+      for (int k = 0; k < 16; ++k) acc[k] = __builtin_fmaf(w, vv[k], acc[k]);
       __builtin_amdgcn_sched_barrier(0);
     }
     m = mb;
   };
-  if (early) {
-    if (j0 < end) process(j0);
-    j0 += KB * AG;
-  }
-  for (bool first = true; j0 < end; j0 += KB * AG, first = false) {
-    if (LDSV && !first) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
+  // the first pass outside the loop: its loads were issued early (cross, register form) or are issued before the new
+  // token's work (self)
+  if (!early && j0 < end) load_pass(j0, end);
+  if (fresh) new_token();
+  if (j0 < end) process(j0);
+  j0 += KB * AG;
+  for (; j0 < end; j0 += KB * AG) {
+    if constexpr (LDSV) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
     load_pass(j0, end);
     process(j0);
   }
-  // LDSV: every wave is done reading its values (and an early pass has landed) before the buffer holds the partial
-  // outputs
+  // LDSV: every wave is done reading its values before the buffer holds the partial outputs
   if constexpr (LDSV) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
