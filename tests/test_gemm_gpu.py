@@ -224,6 +224,40 @@ def test_sparse_equals_dense_on_pruned(ext, M, N, K, group):
     assert torch.equal(xs_, xd_)
 
 
+@pytest.mark.parametrize("M,K", [(300, 1280), (300, 1152), (129, 128), (64, 256), (200, 384), (1000, 5120),
+                                 (300, 4992)])
+def test_sparse_every_tile_same_bits(ext, M, K):
+    """Every gfx950 tile of the 2:4 kernel (the in-workgroup K split among them) gives the int32 sums of the dense
+    product on the pruned weights, and the bias and residual epilogues' bits; K of 1 to 40 stages, odd and even."""
+    from kernels.cuda_ext import EPI_BIAS, EPI_I32, EPI_RESID
+
+    N = 256 if K > 4096 else 512
+    _, xq, xs, _, _, _ = _prep(M, N, K, seed=21 + K)
+    wq, ws, wc, e, b = _sparse_weights(N, K, seed=22 + M)
+    ref_acc = _int_mm_cpu(xq, wq)
+    ref_out = O.gemm_i8(_np(xq), _np(xs), K, _np(wq), _np(ws), bf16_bits(b.cpu()), O.EPI_BIAS)
+    r = torch.randn(M, N, generator=torch.Generator().manual_seed(23)).to(torch.bfloat16).cuda()
+    ref_res = O.gemm_i8(_np(xq), _np(xs), K, _np(wq), _np(ws), bf16_bits(b.cpu()), O.EPI_RESID, resid=bf16_bits(r.cpu()),
+                        alpha=0.5)
+    n_tiles = ext.set_gemm_tile(-1)
+    try:
+        for tile in range(n_tiles):
+            print(f"gemm_sp tile {tile} M={M} K={K}", flush=True)
+            ext.set_gemm_tile(tile)
+            acc = torch.zeros(M, N, dtype=torch.int32, device="cuda")
+            ext.gemm_sp_epi(xq, xs, K, wc, e, ws, b, acc, EPI_I32, None, 1.0, None, -1)
+            out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+            ext.gemm_sp_epi(xq, xs, K, wc, e, ws, b, out, EPI_BIAS, None, 1.0, None, -1)
+            res = r.clone()
+            ext.gemm_sp_epi(xq, xs, K, wc, e, ws, b, res, EPI_RESID, res, 0.5, None, -1)
+            torch.cuda.synchronize()
+            assert np.array_equal(_np(acc), ref_acc), f"tile {tile}"
+            assert np.array_equal(bf16_bits(out), ref_out), f"tile {tile}"
+            assert np.array_equal(bf16_bits(res), ref_res), f"tile {tile}"
+    finally:
+        ext.set_gemm_tile(-1)
+
+
 def test_sparse_silu_q8_equals_dense(ext):
     from kernels.cuda_ext import EPI_SILU_Q8
 
