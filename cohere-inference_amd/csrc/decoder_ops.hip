@@ -207,13 +207,14 @@ dec_attention_kernel(const DecAttnArgs p) {
   // 32-bit offsets from the layer's cache base (a layer's cache stays below 2^32 elements), so that the loads take
   // the uniform base in scalar registers and one offset register each
   const uint32_t vrow0 = (uint32_t)vec0;
-  // key slot i of a pass is live for the wave while its first group's key j0w + i * AG is below the limit (the
+  // key slot i of a pass is live for the wave while its first group's key j0w + i * AG is below the end (the
   // wave's groups are consecutive, so the others' keys of that slot are past it too): slots past the end for the
-  // whole wave are neither loaded nor computed (a scalar branch; short caches do a fraction of a pass)
+  // whole wave are not computed (a scalar branch; short caches do a fraction of a pass). They are still loaded (key 0
+  // of the slot: one cache line for the wave), so that the loads in flight are the same count everywhere and each
+  // key waits only for its own load.
   auto wave_first = [&](int j0) { return __builtin_amdgcn_readfirstlane(j0 - (grp & 7)); };
   // issue order: the scales, the keys, then the values
   auto load_pass = [&](int j0, int limit) {
-    const int j0w = wave_first(j0);
     if constexpr (Q8) {  // byte offsets in 32 bits: the loads then use the scalar base (one offset register each)
       const int jj = j0 + gl * AG;
       const uint32_t off = (vrow0 + (uint32_t)(jj < limit ? jj : 0)) << 2;
@@ -222,7 +223,6 @@ dec_attention_kernel(const DecAttnArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
-      if (j0w + i * AG >= limit) break;
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (Q8) {
@@ -234,7 +234,6 @@ dec_attention_kernel(const DecAttnArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
-      if (j0w + i * AG >= limit) break;
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (!LDSV) {
@@ -365,14 +364,12 @@ dec_attention_kernel(const DecAttnArgs p) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] *= a;
     const float ew = Q8 ? e * vsl : e;  // int8: the value's scale goes into the weight
-    // LDSV with every slot live: value i has landed in LDS once at most the younger copies are still in flight
-    // (stores issued later only make the wait longer); with fewer live slots, all of them
-    const bool full = j0w + (KB - 1) * AG < end;
-    if (LDSV && !full) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       if (j0w + i * AG >= end) break;
-      if (LDSV && full) wait_vm_upto((KB - 1 - i) * VB);
+      // LDSV: value i has landed in LDS once at most the younger copies are still in flight (stores issued later
+      // only make the wait longer)
+      if constexpr (LDSV) wait_vm_upto((KB - 1 - i) * VB);
       const float w = group8_bcast(ew, KB == 8 ? i : 2 * i);
       float vv[16];
       read_v(i, vv);
