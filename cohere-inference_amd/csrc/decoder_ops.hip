@@ -181,9 +181,13 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
 // copy and read-back add latency). The launch takes LDSV when the grid has more workgroups than the GPU has CUs (64
 // rows x 8 heads: one round of 512 workgroups instead of two), the register form otherwise. After the keys, the LDS
 // buffer holds the groups' partial outputs.
-template <bool SELF, bool Q8, bool LDSV>
+// EARLY (cross-attention, register form, one split): the first pass's loads are issued before the slot's frame count
+// is read. A template parameter, not a run-time choice: two ways into the first pass would make the compiler wait
+// for every load in flight where they join.
+template <bool SELF, bool Q8, bool LDSV, bool EARLY = false>
 __global__ void __launch_bounds__(AG * 8) __attribute__((amdgpu_waves_per_eu(LDSV ? 4 : 1)))
 dec_attention_kernel(const DecAttnArgs p) {
+  static_assert(!EARLY || (!SELF && !LDSV), "the early pass is the register form's cross-attention");
   constexpr int KB = Q8 ? 8 : 4;  // keys per group per pass
   constexpr int VB = Q8 ? 1 : 2;  // 16-byte value chunks per lane per key
   constexpr int VBYTES = LDSV ? KB * VB * 8 * 1024 : 0, CBYTES = AG * (HD + 4) * 4;
@@ -194,8 +198,15 @@ dec_attention_kernel(const DecAttnArgs p) {
   const int r = blockIdx.x, h = blockIdx.y, sp = blockIdx.z, nsp = gridDim.z;
   const int s = p.active[r];
   const int tid = threadIdx.x, grp = tid >> 3, gl = tid & 7, wave = tid >> 6, wl = tid & 63;
+  // the query as loaded: converted once the first pass's loads are issued (a conversion ahead of them would make the
+  // wave wait for the query before issuing the keys)
+  uint4 qr[2];
+  {
+    const uint16_t* qp = p.q + (int64_t)r * p.ldq + h * HD + gl * 16;
+    qr[0] = *reinterpret_cast<const uint4*>(qp);
+    qr[1] = *reinterpret_cast<const uint4*>(qp + 8);
+  }
   float q[16];
-  load16_bf(p.q + (int64_t)r * p.ldq + h * HD + gl * 16, q);
   const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
   // LDSV: the wave's LDS block for pass key i, value chunk c (64 lanes x 16 bytes; lane wl's slot at + 16 wl)
   auto vblock = [&](int i, int c) { return sbuf + ((i * VB + c) * 8 + wave) * 1024; };
@@ -232,6 +243,7 @@ dec_attention_kernel(const DecAttnArgs p) {
         kr[i][1] = *reinterpret_cast<const uint4*>(p.k + (vec * HD + gl * 16 + 8));
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // the keys' loads stay ahead of the values': a key waits for keys only
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const int jj = j0 + i * AG;
@@ -251,6 +263,7 @@ dec_attention_kernel(const DecAttnArgs p) {
         __builtin_amdgcn_global_load_lds(src + 8, (LDS_AS void*)vblock(i, 1), 16, 0, 0);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // nothing that waits for a load is scheduled among the pass's loads
   };
   auto read_v = [&](int i, float (&vv)[16]) {
     uint4 a, b;
@@ -268,7 +281,7 @@ dec_attention_kernel(const DecAttnArgs p) {
   // cache's T frames, masked by the length after), so the key loads do not wait for it; the frame count is close to
   // T anyway. Self-attention lengths grow from 1, so there the length is waited for. (In the LDS form the early pass
   // kept the loaded keys live across the length load and made the kernel spill.)
-  const bool early = !LDSV && !SELF && nsp == 1;
+  constexpr bool early = EARLY;
   if (early) load_pass(grp, p.T);
   const int n = p.n[s];
   float m = -INFINITY, l = 0.f, acc[16];
@@ -381,7 +394,10 @@ dec_attention_kernel(const DecAttnArgs p) {
   };
   // the first pass outside the loop: its loads were issued early (cross, register form) or are issued before the new
   // token's work (self)
-  if (!early && j0 < end) load_pass(j0, end);
+  // (for every lane, even past the end: the loads clamp their keys, and a load inside a branch would leave the
+  // compiler unable to count the loads in flight after it)
+  if (!early) load_pass(j0, end);
+  unpack_bf(qr[0], qr[1], q);
   if (fresh) new_token();
   if (j0 < end) process(j0);
   j0 += KB * AG;
@@ -701,6 +717,9 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
   (ldsv ? (dec_attention_kernel<SELF_, Q8_, true><<<grid, AG * 8, 0, s>>>(p), 0)                  \
         : (dec_attention_kernel<SELF_, Q8_, false><<<grid, AG * 8, 0, s>>>(p), 0))
   if (self) q8 ? COHERE_ATT(true, true) : COHERE_ATT(true, false);
+  else if (!ldsv && splits == 1)
+    q8 ? dec_attention_kernel<false, true, false, true><<<grid, AG * 8, 0, s>>>(p)
+       : dec_attention_kernel<false, false, false, true><<<grid, AG * 8, 0, s>>>(p);
   else q8 ? COHERE_ATT(false, true) : COHERE_ATT(false, false);
 #undef COHERE_ATT
   if (splits > 1) dec_combine_kernel<<<dim3((unsigned)rows, (unsigned)p.H), HD, 0, s>>>(p.part, (int)splits, p.out, p.H);
