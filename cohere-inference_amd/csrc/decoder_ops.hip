@@ -178,8 +178,9 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
 // LDSV selects where a pass's values wait for the softmax weights: in registers (values loaded with the keys; ~200
 // VGPRs, one 512-thread workgroup per CU) or in LDS, copied global -> LDS by the load unit (global_load_lds), each
 // lane's 16-byte chunks into its own slots and read back by the same lane (<= 128 VGPRs, two workgroups per CU; the
-// copy and read-back add latency). The launch takes LDSV when the grid has more workgroups than the GPU has CUs (64
-// rows x 8 heads: one round of 512 workgroups instead of two), the register form otherwise. After the keys, the LDS
+// copy and read-back add latency). Self-attention takes LDSV when the grid has more workgroups than the GPU has CUs
+// (64 rows x 8 heads: one round of 512 workgroups instead of two), the register form otherwise; cross-attention with
+// one split always takes the register form (its early pass outweighs the second round). After the keys, the LDS
 // buffer holds the groups' partial outputs.
 // EARLY (cross-attention, register form, one split): the first pass's loads are issued before the slot's frame count
 // is read. A template parameter, not a run-time choice: two ways into the first pass would make the compiler wait
@@ -716,8 +717,11 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
 #define COHERE_ATT(SELF_, Q8_)                                                                    \
   (ldsv ? (dec_attention_kernel<SELF_, Q8_, true><<<grid, AG * 8, 0, s>>>(p), 0)                  \
         : (dec_attention_kernel<SELF_, Q8_, false><<<grid, AG * 8, 0, s>>>(p), 0))
+  // cross-attention with one split always takes the register form with its early pass: at 64 rows x 8 heads (two
+  // rounds of workgroups) 12.0 us against 13.6 in the LDS form; self-attention keeps the LDS form there (11.6 us
+  // against 12.6)
   if (self) q8 ? COHERE_ATT(true, true) : COHERE_ATT(true, false);
-  else if (!ldsv && splits == 1)
+  else if (splits == 1)
     q8 ? dec_attention_kernel<false, true, false, true><<<grid, AG * 8, 0, s>>>(p)
        : dec_attention_kernel<false, false, false, true><<<grid, AG * 8, 0, s>>>(p);
   else q8 ? COHERE_ATT(false, true) : COHERE_ATT(false, false);
