@@ -142,6 +142,46 @@ def test_dec_attention_long_caches(gpu, q8, self_attn):
     _close(bf16_bits(out), want)
 
 
+@pytest.mark.parametrize("q8", [True, False])
+@pytest.mark.parametrize("self_attn,splits", [(True, 1), (False, 1), (False, 2)])
+def test_dec_attention_many_rows(gpu, q8, self_attn, splits):
+    """40 rows x 8 heads: more workgroups than CUs, so self-attention takes the LDS form (values copied into LDS) and
+    split cross-attention too, while unsplit cross-attention takes the register form with its early pass; lengths on
+    the 64-key group boundaries, 0 (self: the new token alone) and 448, against the checker."""
+    g = torch.Generator().manual_seed(31 + 2 * q8 + self_attn + 4 * splits)
+    rows, H, T = 40, 8, 465
+    slots = rows + 1
+    active = torch.randperm(slots, generator=g)[:rows].int()
+    edge = [0, 1, 63, 64, 65, 448] if self_attn else [1, 63, 64, 65, 375, 465]
+    n = torch.randint(1, 449 if self_attn else T + 1, (slots,), generator=g).int()
+    n[active[:len(edge)].long()] = torch.tensor(edge, dtype=torch.int32)
+    q = torch.randn(rows, (3 if self_attn else 1) * H * 128, generator=g).to(torch.bfloat16)
+    out = torch.empty(rows, H * 128, dtype=torch.bfloat16, device=gpu)
+    part = torch.empty(rows * H * splits * 130, device=gpu)
+    print(f"dec_attention rows={rows} q8={q8} self={self_attn} splits={splits}", flush=True)
+    if q8:
+        k8, v8, ks, vs = _caches(g, slots, H, T)
+        gk, gv, gks, gvs = (t.to(gpu) for t in (k8, v8, ks, vs))
+        _ext().dec_attention_q8(self_attn, active.to(gpu), q.to(gpu), gk, gv, gks, gvs, n.to(gpu), 128 ** -0.5,
+                                splits, part, out)
+        ck, cv, cks, cvs = (t.numpy().copy() for t in (k8, v8, ks, vs))
+        want = oracle.dec_attention(self_attn, active.numpy(), _bf(q), n.numpy(), 128 ** -0.5, k8=ck, v8=cv,
+                                    ks=cks, vs=cvs)
+        if self_attn:
+            assert np.array_equal(gk.cpu().numpy(), ck) and np.array_equal(gv.cpu().numpy(), cv)
+            assert np.array_equal(gks.cpu().numpy(), cks) and np.array_equal(gvs.cpu().numpy(), cvs)
+    else:
+        k = torch.randn(slots, H, T, 128, generator=g).to(torch.bfloat16)
+        v = torch.randn(slots, H, T, 128, generator=g).to(torch.bfloat16)
+        gk, gv = k.to(gpu), v.to(gpu)
+        _ext().dec_attention(self_attn, active.to(gpu), q.to(gpu), gk, gv, n.to(gpu), 0.05, splits, part, out)
+        ck, cv = bf16_bits(k).copy(), bf16_bits(v).copy()
+        want = oracle.dec_attention(self_attn, active.numpy(), _bf(q), n.numpy(), 0.05, k=ck, v=cv)
+        if self_attn:
+            assert np.array_equal(bf16_bits(gk), ck) and np.array_equal(bf16_bits(gv), cv)
+    _close(bf16_bits(out), want)
+
+
 def test_dec_pick_exact(gpu):
     g = torch.Generator().manual_seed(8)
     rows, V, S = 7, 16384, 10
