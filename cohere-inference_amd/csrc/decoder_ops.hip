@@ -82,10 +82,10 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
 // ---- attention of one new token per row ---------------------------------------------------------------------------
 // A workgroup of 512 threads per (row, head, split): 64 groups of 8 lanes, each lane 16 of the 128 dims, each group
 // taking every 64th key of the split, 8 (int8) or 4 (bf16) keys per pass with all their loads in flight at once (a
-// whole 448-token self cache or 375-frame cross cache in one memory round trip). Per
-// key the group's partial dot products meet through three lane shuffles; the online softmax runs in fp32 per group,
-// one rescale per pass; the 64 groups are combined through LDS at the end (or, with several splits, written as
-// partials (o[128], max, sum) for dec_combine).
+// whole 448-token self cache or 375-frame cross cache in one memory round trip). A pass's partial dot products meet
+// in one transposed reduction over the group's lanes (lane gl ends with key gl's); the online softmax runs in fp32
+// per group, one rescale per pass; the 64 groups are combined through LDS at the end (or, with several splits,
+// written as partials (o[128], max, sum) for dec_combine).
 struct DecAttnArgs {
   const int32_t* active;
   const uint16_t* q;  // (rows, ldq): head h at column h * 128 (self: q | k | v of the new token)
