@@ -139,14 +139,14 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
     if constexpr (LN) {
       if (first) {
         // every wave reaches this (the caller guarantees at least NW blocks of K)
+        // rows_pre is a ring of PRE rows in flight: row j + PRE is issued before row j is normalised, so with more
+        // rows than PRE per wave their loads overlap the LayerNorms instead of each waiting a round trip of its own
 #pragma unroll
         for (int j = 0; j < RPW; ++j) {
-          cohere_rows::Row<2> r;
-          if (j < PRE) {
-            r = rows_pre[j];
-          } else {
-            const int m = min(m_base + wave * RPW + j, p.M - 1);
-            cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, r);
+          cohere_rows::Row<2> r = rows_pre[j % PRE];
+          if (j + PRE < RPW) {
+            const int m = min(m_base + wave * RPW + j + PRE, p.M - 1);
+            cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j % PRE]);
           }
           cohere_rows::ln_row<2>(r, p.K, lane, lnp, p.eps);
           cohere_rows::store_row<2>(r, p.K, lane, reinterpret_cast<uint16_t*>(smem + (wave * RPW + j) * LN_ROW));
