@@ -81,7 +81,7 @@ __global__ void __launch_bounds__(256) dec_add_ln_kernel(uint16_t* __restrict__ 
 
 // ---- attention of one new token per row ---------------------------------------------------------------------------
 // A workgroup of 512 threads per (row, head, split): 64 groups of 8 lanes, each lane 16 of the 128 dims, each group
-// taking every 64th key of the split, 8 (int8) or 4 (bf16) keys per pass with all their loads in flight at once (a
+// taking every 64th key of the split, 7 (int8) or 4 (bf16) keys per pass with all their loads in flight at once (a
 // whole 448-token self cache or 375-frame cross cache in one memory round trip). A pass's partial dot products meet
 // in one transposed reduction over the group's lanes (lane gl ends with key gl's); the online softmax runs in fp32
 // per group, one rescale per pass; the 64 groups are combined through LDS at the end (or, with several splits,
@@ -103,7 +103,7 @@ struct DecAttnArgs {
   float* part;        // (rows, H, splits, 130) when split
 };
 
-constexpr int AG = 64;  // key groups per workgroup (8 lanes each: 512 threads; one pass covers 512 int8 keys)
+constexpr int AG = 64;  // key groups per workgroup (8 lanes each: 512 threads; one pass covers 448 int8 keys)
 
 DEVI void load16_bf(const uint16_t* p, float (&f)[16]) {
   const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
@@ -175,13 +175,12 @@ DEVI void attend_one(const float (&q)[16], const float (&kk)[16], const float (&
   m = mn;
 }
 
-// LDSV selects where a pass's values wait for the softmax weights: in registers (values loaded with the keys; ~200
-// VGPRs, one 512-thread workgroup per CU) or in LDS, copied global -> LDS by the load unit (global_load_lds), each
-// lane's 16-byte chunks into its own slots and read back by the same lane (<= 128 VGPRs, two workgroups per CU; the
-// copy and read-back add latency). Self-attention takes LDSV when the grid has more workgroups than the GPU has CUs
-// (64 rows x 8 heads: one round of 512 workgroups instead of two), the register form otherwise; cross-attention with
-// one split always takes the register form (its early pass outweighs the second round). After the keys, the LDS
-// buffer holds the groups' partial outputs.
+// LDSV selects where a pass's values wait for the softmax weights: in registers (values loaded with the keys) or in
+// LDS, copied global -> LDS by the load unit (global_load_lds), each lane's 16-byte chunks into its own slots and read
+// back by the same lane (the copy and read-back add latency, and with copies into LDS and register loads both in
+// flight the compiler waits for all of them before the first key). The register form fits two workgroups per CU (113-123 VGPRs with 7 key slots per
+// pass) and lets each key and value wait for its own load only; LDSV is taken only by split launches whose grid has
+// more workgroups than the GPU has CUs. After the keys, the LDS buffer holds the groups' partial outputs.
 // EARLY (cross-attention, register form, one split): the first pass's loads are issued before the slot's frame count
 // is read. A template parameter, not a run-time choice: two ways into the first pass would make the compiler wait
 // for every load in flight where they join.
@@ -189,9 +188,12 @@ template <bool SELF, bool Q8, bool LDSV, bool EARLY = false>
 __global__ void __launch_bounds__(AG * 8) __attribute__((amdgpu_waves_per_eu(LDSV ? 4 : 1)))
 dec_attention_kernel(const DecAttnArgs p) {
   static_assert(!EARLY || (!SELF && !LDSV), "the early pass is the register form's cross-attention");
-  constexpr int KB = Q8 ? 8 : 4;  // keys per group per pass
+  // key slots per group per pass: KL loaded (int8: 7, so that a pass covers 448 keys, the decoder's longest caches,
+  // and the register form fits two workgroups per CU), KB in the lanes' reduction (a power of two; slots KL..KB-1
+  // are never live)
+  constexpr int KB = Q8 ? 8 : 4, KL = Q8 ? 7 : 4;
   constexpr int VB = Q8 ? 1 : 2;  // 16-byte value chunks per lane per key
-  constexpr int VBYTES = LDSV ? KB * VB * 8 * 1024 : 0, CBYTES = AG * (HD + 4) * 4;
+  constexpr int VBYTES = LDSV ? KL * VB * 8 * 1024 : 0, CBYTES = AG * (HD + 4) * 4;
   __shared__ __attribute__((aligned(16))) char sbuf[VBYTES > CBYTES ? VBYTES : CBYTES];
   __shared__ float sm[AG], sl[AG], sw[AG], sML[2];
   __shared__ float spart[4][HD];
@@ -211,7 +213,7 @@ dec_attention_kernel(const DecAttnArgs p) {
   const int64_t vec0 = ((int64_t)s * p.H + h) * p.T;  // index of key 0's 128-vector
   // LDSV: the wave's LDS block for pass key i, value chunk c (64 lanes x 16 bytes; lane wl's slot at + 16 wl)
   auto vblock = [&](int i, int c) { return sbuf + ((i * VB + c) * 8 + wave) * 1024; };
-  uint4 kr[KB][Q8 ? 1 : 2], vr[LDSV ? 1 : KB][Q8 ? 1 : 2];
+  uint4 kr[KL][Q8 ? 1 : 2], vr[LDSV ? 1 : KL][Q8 ? 1 : 2];
   // int8 scales: lane gl of a group loads the scales of the group's key gl of the pass (one load each for the key
   // and value scales, where one load per key made 16 narrow loads per lane): the lane that ends up with that key's
   // dot product
@@ -234,7 +236,7 @@ dec_attention_kernel(const DecAttnArgs p) {
       vsl = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.vs) + off);
     }
 #pragma unroll
-    for (int i = 0; i < KB; ++i) {
+    for (int i = 0; i < KL; ++i) {
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (Q8) {
@@ -246,7 +248,7 @@ dec_attention_kernel(const DecAttnArgs p) {
     }
     __builtin_amdgcn_sched_barrier(0);  // the keys' loads stay ahead of the values': a key waits for keys only
 #pragma unroll
-    for (int i = 0; i < KB; ++i) {
+    for (int i = 0; i < KL; ++i) {
       const int jj = j0 + i * AG;
       const uint32_t vec = vrow0 + (uint32_t)(jj < limit ? jj : 0);
       if constexpr (!LDSV) {
@@ -319,11 +321,11 @@ dec_attention_kernel(const DecAttnArgs p) {
     attend_one(q, kn, vn, p.scale, m, l, acc);
   };
   const int chunk = (n + nsp - 1) / nsp, start = sp * chunk, end = min(n, start + chunk);
-  // each group takes KB keys per pass (every 64th key), all loads issued before any use: one memory round trip per
+  // each group takes KL keys per pass (every 64th key), all loads issued before any use: one memory round trip per
   // pass; then one softmax update for the pass
   int j0 = start + grp;
-  // a pass's loads are issued at the top of the pass: no registers carry loaded keys across passes, so one pass of KB
-  // keys per group fits the register budget. Caches of more than KB * AG = 512 keys pay one more memory round trip
+  // a pass's loads are issued at the top of the pass: no registers carry loaded keys across passes, so one pass of KL
+  // keys per group fits the register budget. Caches of more than KL * AG = 448 keys pay one more memory round trip
   // per pass. One pass over the loaded keys is a lambda, so that the early pass runs outside the loop (a loop whose
   // first pass could come from registers loaded before it made the compiler copy every loaded register at its back
   // edge).
@@ -339,7 +341,7 @@ dec_attention_kernel(const DecAttnArgs p) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       d[i] = 0.f;
-      if (j0w + i * AG >= end) continue;
+      if (i >= KL || j0w + i * AG >= end) continue;
       float kk[16];
       if constexpr (Q8) unpack_q8(kr[i][0], 1.f, kk);  // the integers; the key's scale multiplies the dot product
       else unpack_bf(kr[i][0], kr[i][1], kk);
@@ -371,7 +373,7 @@ dec_attention_kernel(const DecAttnArgs p) {
       dk = d2[0] + dpp_mov<DPP_XOR1>(d2[0]);  // both lanes of a pair hold the key's sum
     }
     if constexpr (Q8) dk *= ksl;
-    const float sc = j0 + kx * AG < end ? dk * p.scale : -INFINITY;
+    const float sc = kx < KL && j0 + kx * AG < end ? dk * p.scale : -INFINITY;
     const float mb = fmaxf(m, group_max(sc));
     const float a = __expf(m - mb), e = __expf(sc - mb);
     l = __builtin_fmaf(l, a, group_sum(KB == 8 || !hi1 ? e : 0.f));
@@ -379,11 +381,11 @@ dec_attention_kernel(const DecAttnArgs p) {
     for (int k = 0; k < 16; ++k) acc[k] *= a;
     const float ew = Q8 ? e * vsl : e;  // int8: the value's scale goes into the weight
 #pragma unroll
-    for (int i = 0; i < KB; ++i) {
+    for (int i = 0; i < KL; ++i) {
       if (j0w + i * AG >= end) break;
       // LDSV: value i has landed in LDS once at most the younger copies are still in flight (stores issued later
       // only make the wait longer)
-      if constexpr (LDSV) wait_vm_upto((KB - 1 - i) * VB);
+      if constexpr (LDSV) wait_vm_upto((KL - 1 - i) * VB);
       const float w = group8_bcast(ew, KB == 8 ? i : 2 * i);
       float vv[16];
       read_v(i, vv);
@@ -401,8 +403,8 @@ dec_attention_kernel(const DecAttnArgs p) {
   unpack_bf(qr[0], qr[1], q);
   if (fresh) new_token();
   if (j0 < end) process(j0);
-  j0 += KB * AG;
-  for (; j0 < end; j0 += KB * AG) {
+  j0 += KL * AG;
+  for (; j0 < end; j0 += KL * AG) {
     if constexpr (LDSV) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // last pass's value reads are done
     load_pass(j0, end);
     process(j0);
@@ -713,13 +715,13 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
   if (rows == 0) return 0;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)rows, (unsigned)p.H, (unsigned)splits);
-  const bool ldsv = rows * p.H * splits > num_cus();
+  // the register form (two workgroups per CU at <= 128 VGPRs, each key and value waiting only for its own load)
+  // unless the launch is split over more workgroups than the GPU has CUs: at 64 rows x 8 heads self-attention takes
+  // 10.5 us there against 11.7 in the LDS form, cross-attention (with its early pass) 12.0 against 13.6
+  const bool ldsv = splits > 1 && rows * p.H * splits > num_cus();
 #define COHERE_ATT(SELF_, Q8_)                                                                    \
   (ldsv ? (dec_attention_kernel<SELF_, Q8_, true><<<grid, AG * 8, 0, s>>>(p), 0)                  \
         : (dec_attention_kernel<SELF_, Q8_, false><<<grid, AG * 8, 0, s>>>(p), 0))
-  // cross-attention with one split always takes the register form with its early pass: at 64 rows x 8 heads (two
-  // rounds of workgroups) 12.0 us against 13.6 in the LDS form; self-attention keeps the LDS form there (11.6 us
-  // against 12.6)
   if (self) q8 ? COHERE_ATT(true, true) : COHERE_ATT(true, false);
   else if (splits == 1)
     q8 ? dec_attention_kernel<false, true, false, true><<<grid, AG * 8, 0, s>>>(p)

@@ -143,11 +143,11 @@ def test_dec_attention_long_caches(gpu, q8, self_attn):
 
 
 @pytest.mark.parametrize("q8", [True, False])
-@pytest.mark.parametrize("self_attn,splits", [(True, 1), (False, 1), (False, 2)])
+@pytest.mark.parametrize("self_attn,splits", [(True, 1), (True, 2), (False, 1), (False, 2)])
 def test_dec_attention_many_rows(gpu, q8, self_attn, splits):
-    """40 rows x 8 heads: more workgroups than CUs, so self-attention takes the LDS form (values copied into LDS) and
-    split cross-attention too, while unsplit cross-attention takes the register form with its early pass; lengths on
-    the 64-key group boundaries, 0 (self: the new token alone) and 448, against the checker."""
+    """40 rows x 8 heads: unsplit, the register form (two workgroups per CU; cross-attention with its early pass);
+    split in two, more workgroups than CUs, so the LDS form (values copied into LDS); lengths on the 64-key group
+    boundaries, 0 (self: the new token alone) and 448, against the checker."""
     g = torch.Generator().manual_seed(31 + 2 * q8 + self_attn + 4 * splits)
     rows, H, T = 40, 8, 465
     slots = rows + 1
