@@ -105,23 +105,6 @@ struct DecAttnArgs {
 
 constexpr int AG = 64;  // key groups per workgroup (8 lanes each: 512 threads; one pass covers 448 int8 keys)
 
-DEVI void load16_bf(const uint16_t* p, float (&f)[16]) {
-  const uint4 a = *reinterpret_cast<const uint4*>(p), b = *reinterpret_cast<const uint4*>(p + 8);
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    f[2 * k] = __uint_as_float(w[k] << 16);
-    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-  }
-}
-
-DEVI void load16_q8(const int8_t* p, float s, float (&f)[16]) {
-  const uint4 u = *reinterpret_cast<const uint4*>(p);
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int k = 0; k < 16; ++k) f[k] = (float)(int8_t)((w[k >> 2] >> (8 * (k & 3))) & 0xff) * s;
-}
-
 DEVI void unpack_q8(const uint4& u, float s, float (&f)[16]) {
   const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
