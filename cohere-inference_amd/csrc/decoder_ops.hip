@@ -482,6 +482,18 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
   const int r = blockIdx.x, tid = threadIdx.x;
   const int s = active[r];  // a padding row (the dummy slot) is scanned too and then dropped: its loads do not wait
   const uint16_t* row = logits + (int64_t)r * V;
+  // the slot's state, loaded now by the lane that updates it, so that after the scan only the chosen token's
+  // embedding is a round trip of its own
+  int64_t tok0 = 0, forced0 = 0;
+  int pos0 = 0, plen0 = 0, lim0 = 0;
+  uint8_t fin0 = 1;
+  if (tid == 0) {
+    fin0 = finished[s];
+    pos0 = pos[s];
+    plen0 = plen[s];
+    lim0 = limit[s];
+    if constexpr (EVEC > 0) tok0 = tok[s];
+  }
   float best = -INFINITY;
   int arg = 0x7fffffff;
   // eight 16-byte loads per thread in flight at once (a 16384-entry row in one memory round trip), then the scan in
@@ -495,6 +507,8 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
       u[j] = i < V ? *reinterpret_cast<const uint4*>(row + i) : make_uint4(0xff80ff80u, 0xff80ff80u, 0xff80ff80u,
                                                                            0xff80ff80u);  // -inf: never picked
     }
+    // the forced token at the next position (used only inside the prompt, so its index is clamped to the row)
+    if (tid == 0 && i0 == 0) forced0 = forced[(int64_t)s * FP + min(pos0 + 1, FP - 1)];
 #pragma unroll
     for (int j = 0; j < LB; ++j) {
       const uint32_t w[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
@@ -544,19 +558,19 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
   __shared__ int64_t s_tok;
   __shared__ int s_pos;
   if (tid == 0) {
-    int64_t t_next = EVEC > 0 ? tok[s] : 0;
-    int p_next = EVEC > 0 ? pos[s] : 0;
+    int64_t t_next = tok0;
+    int p_next = EVEC > 0 ? pos0 : 0;
     // ended at an earlier step (or the dummy slot): nothing moves until the host retires the slot
-    if (s != dummy && !finished[s]) {
+    if (s != dummy && !fin0) {
       for (int w = 1; w < 4; ++w)
         if (sb[w] > best || (sb[w] == best && sa[w] < arg)) {
           best = sb[w];
           arg = sa[w];
         }
-      const int at = pos[s] + 1;
-      const bool in_prompt = at < plen[s];
-      const int64_t nt = in_prompt ? forced[(int64_t)s * FP + at] : (int64_t)arg;
-      const uint8_t fin = (!in_prompt && (nt == eos || at >= limit[s])) ? 1 : 0;
+      const int at = pos0 + 1;
+      const bool in_prompt = at < plen0;
+      const int64_t nt = in_prompt ? forced0 : (int64_t)arg;
+      const uint8_t fin = (!in_prompt && (nt == eos || at >= lim0)) ? 1 : 0;
       out[(int64_t)s * OUT + at] = nt;
       tok[s] = nt;
       pos[s] = at;
