@@ -182,6 +182,32 @@ def test_dec_attention_many_rows(gpu, q8, self_attn, splits):
     _close(bf16_bits(out), want)
 
 
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_dec_attention_sixteen_heads(gpu, self_attn):
+    """16 heads (the kernels take any head count; the decoders here have 8): 20 rows, int8 caches, against the
+    checker, with the new key and value of self-attention written bit for bit."""
+    g = torch.Generator().manual_seed(41 + self_attn)
+    rows, H, T = 20, 16, 200
+    slots = rows + 1
+    active = torch.randperm(slots, generator=g)[:rows].int()
+    n = torch.randint(0, 199 if self_attn else T + 1, (slots,), generator=g).int()
+    if not self_attn:
+        n = n.clamp(min=1)
+    q = torch.randn(rows, (3 if self_attn else 1) * H * 128, generator=g).to(torch.bfloat16)
+    out = torch.empty(rows, H * 128, dtype=torch.bfloat16, device=gpu)
+    k8, v8, ks, vs = _caches(g, slots, H, T)
+    gk, gv, gks, gvs = (t.to(gpu) for t in (k8, v8, ks, vs))
+    _ext().dec_attention_q8(self_attn, active.to(gpu), q.to(gpu), gk, gv, gks, gvs, n.to(gpu), 128 ** -0.5, 1, None,
+                            out)
+    ck, cv, cks, cvs = (t.numpy().copy() for t in (k8, v8, ks, vs))
+    want = oracle.dec_attention(self_attn, active.numpy(), _bf(q), n.numpy(), 128 ** -0.5, k8=ck, v8=cv, ks=cks,
+                                vs=cvs)
+    _close(bf16_bits(out), want)
+    if self_attn:
+        assert np.array_equal(gk.cpu().numpy(), ck) and np.array_equal(gv.cpu().numpy(), cv)
+        assert np.array_equal(gks.cpu().numpy(), cks) and np.array_equal(gvs.cpu().numpy(), cvs)
+
+
 def test_dec_pick_exact(gpu):
     g = torch.Generator().manual_seed(8)
     rows, V, S = 7, 16384, 10
