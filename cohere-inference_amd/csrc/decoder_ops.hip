@@ -699,10 +699,13 @@ int num_cus() {
   return n;
 }
 
-int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t splits, int64_t part_len,
-                    void* stream, const char* name) {
+int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t slots, int64_t splits,
+                    int64_t part_len, void* stream, const char* name) {
   const std::string nm(name);
   COHERE_REQUIRE(rows >= 0 && p.H > 0 && p.H <= 65535 && p.T > 0 && splits >= 1 && splits <= 64, nm + ": bad sizes");
+  // the kernels address a cache with 32-bit element offsets
+  COHERE_REQUIRE(slots > 0 && slots * (int64_t)p.H * p.T * HD < (int64_t(1) << 32),
+                 nm + ": slots x heads x T x 128 must be positive and below 2^32");
   COHERE_REQUIRE(p.active && p.q && p.n && p.out && al16(p.q) && p.ldq % 8 == 0 && al16(p.out),
                  nm + ": bad pointer");
   COHERE_REQUIRE(q8 ? (p.k8 && p.v8 && p.ks && p.vs && al16(p.k8) && al16(p.v8)) : (p.k && p.v && al16(p.k) && al16(p.v)),
@@ -731,24 +734,25 @@ int attention_entry(bool self, bool q8, DecAttnArgs& p, int64_t rows, int64_t sp
 }  // namespace
 
 extern "C" int cohere_dec_attention(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
-                                    uint16_t* k, uint16_t* v, const int32_t* n, int64_t heads, int64_t T, float scale,
-                                    int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream) {
+                                    uint16_t* k, uint16_t* v, const int32_t* n, int64_t slots, int64_t heads, int64_t T,
+                                    float scale, int64_t splits, float* part, int64_t part_len, uint16_t* out,
+                                    void* stream) {
   cohere::clear_error();
   DecAttnArgs p{};
   p.active = active; p.q = q; p.ldq = ldq; p.k = k; p.v = v; p.n = n; p.H = (int)heads; p.T = (int)T;
   p.scale = scale; p.out = out; p.part = part;
-  return attention_entry(self != 0, false, p, rows, splits, part_len, stream, "dec_attention");
+  return attention_entry(self != 0, false, p, rows, slots, splits, part_len, stream, "dec_attention");
 }
 
 extern "C" int cohere_dec_attention_q8(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q,
                                        int64_t ldq, int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n,
-                                       int64_t heads, int64_t T, float scale, int64_t splits, float* part,
+                                       int64_t slots, int64_t heads, int64_t T, float scale, int64_t splits, float* part,
                                        int64_t part_len, uint16_t* out, void* stream) {
   cohere::clear_error();
   DecAttnArgs p{};
   p.active = active; p.q = q; p.ldq = ldq; p.k8 = k8; p.v8 = v8; p.ks = ks; p.vs = vs; p.n = n; p.H = (int)heads;
   p.T = (int)T; p.scale = scale; p.out = out; p.part = part;
-  return attention_entry(self != 0, true, p, rows, splits, part_len, stream, "dec_attention_q8");
+  return attention_entry(self != 0, true, p, rows, slots, splits, part_len, stream, "dec_attention_q8");
 }
 
 extern "C" int cohere_dec_pick(const uint16_t* logits, int64_t rows, int64_t V, const int32_t* active, int64_t dummy,

@@ -61,8 +61,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "cohere_relpos_attention": [P, P, I64, P, P, P, I64, I64, I64, I64, I64, F, P, P],
         "cohere_dec_embed": [P, I64, P, P, P, P, P, P, F, P, P, F, P, P, I64, P],
         "cohere_dec_add_ln": [P, P, I64, P, P, F, P, I64, I64, P],
-        "cohere_dec_attention": [I32, P, I64, P, I64, P, P, P, I64, I64, F, I64, P, I64, P, P],
-        "cohere_dec_attention_q8": [I32, P, I64, P, I64, P, P, P, P, P, I64, I64, F, I64, P, I64, P, P],
+        "cohere_dec_attention": [I32, P, I64, P, I64, P, P, P, I64, I64, I64, F, I64, P, I64, P, P],
+        "cohere_dec_attention_q8": [I32, P, I64, P, I64, P, P, P, P, P, I64, I64, I64, F, I64, P, I64, P, P],
         "cohere_dec_pick": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P],
         "cohere_dec_pick_embed": [P, I64, I64, P, I64, P, P, P, P, I64, P, P, P, I64, I64, I64, P, P, P, P, F, P, P, F,
                                   P, P, I64, P, P],
@@ -439,7 +439,6 @@ class _Ext:
     def _att_checks(self, q, k, out, part, splits):
         _check(k.dim() == 4 and k.shape[3] == 128 and k.is_contiguous() and q.stride(1) == 1 and out.is_contiguous(),
                "dec_attention: caches (slots, H, T, 128) contiguous, q with unit column stride")
-        _check(k.numel() < 2 ** 32, "dec_attention: a cache of 2^32 or more elements (32-bit offsets in the kernel)")
         rows, H = q.shape[0], k.shape[1]
         _check(splits == 1 or (part is not None and part.numel() >= rows * H * splits * 130),
                "dec_attention: splits > 1 needs part")
@@ -449,7 +448,7 @@ class _Ext:
         """softmax(q k^T scale) v of one new token per row over its slot's bf16 cache (decoder_ops.cu:235-262)."""
         rows, H = self._att_checks(q, k, out, part, splits)
         self._call("cohere_dec_attention", int(bool(self_attn)), _ptr(active), rows, _ptr(q), q.stride(0), _ptr(k),
-                   _ptr(v), _ptr(n), H, k.shape[2], float(scale), int(splits), _ptr(part),
+                   _ptr(v), _ptr(n), k.shape[0], H, k.shape[2], float(scale), int(splits), _ptr(part),
                    part.numel() if part is not None else 0, _ptr(out), _stream())
 
     def dec_attention_q8(self, self_attn, active, q, k8, v8, ks, vs, n, scale, splits, part, out):
@@ -458,7 +457,7 @@ class _Ext:
         _check(k8.dtype == torch.int8 and ks.dtype == torch.float32 and ks.is_contiguous() and vs.is_contiguous(),
                "dec_attention_q8: int8 caches, fp32 scales")
         self._call("cohere_dec_attention_q8", int(bool(self_attn)), _ptr(active), rows, _ptr(q), q.stride(0),
-                   _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs), _ptr(n), H, k8.shape[2], float(scale), int(splits),
+                   _ptr(k8), _ptr(v8), _ptr(ks), _ptr(vs), _ptr(n), k8.shape[0], H, k8.shape[2], float(scale), int(splits),
                    _ptr(part), part.numel() if part is not None else 0, _ptr(out), _stream())
 
     def dec_pick(self, logits, active, dummy, tok, pos, finished, forced, plen, limit, out, pad, eos):

@@ -196,17 +196,23 @@ class EncoderLayer:
 
 
 def metadata(lengths: list[int], device) -> dict:
-    """The packed batch's attention tiles (sequence start, length, first query row, 0) per 64 queries, and each row's
-    sequence range [lo, hi) for the depthwise convolution (reference fast_encoder.py:203-213)."""
-    starts, s = [], 0
-    for n in lengths:
-        starts.append(s)
-        s += n
-    tiles = [(st, n, q0, 0) for st, n in zip(starts, lengths) for q0 in range(0, n, 64)]
-    lo = torch.tensor([st for st, n in zip(starts, lengths) for _ in range(n)], dtype=torch.int32)
-    hi = torch.tensor([st + n for st, n in zip(starts, lengths) for _ in range(n)], dtype=torch.int32)
-    return {"tiles": torch.tensor(tiles, dtype=torch.int32).reshape(-1, 4).to(device),
-            "lo": lo.to(device), "hi": hi.to(device), "max_len": max(lengths) if lengths else 0}
+    """Index tables of a packed batch (reference fast_encoder.py:203-213 defines the format):
+
+    - tiles: int32 (n_tiles, 4), one entry per block of 64 queries of one piece: (first row of the piece, its length,
+      first query of the block within the piece, 0);
+    - lo, hi: int32 (rows,), each packed row's piece as the half-open row range the depthwise convolution may read;
+    - max_len: the longest piece.
+
+    Built with whole-tensor index arithmetic on the host, then copied to the device."""
+    n = torch.tensor(list(lengths), dtype=torch.int64)
+    end = n.cumsum(0)
+    first = end - n
+    blocks = (n + 63) // 64
+    piece = torch.repeat_interleave(torch.arange(len(n)), blocks)
+    block_in_piece = torch.arange(int(blocks.sum())) - torch.repeat_interleave(blocks.cumsum(0) - blocks, blocks)
+    tiles = torch.stack([first[piece], n[piece], 64 * block_in_piece, torch.zeros_like(piece)], 1)
+    return {"tiles": tiles.to(torch.int32).to(device), "lo": torch.repeat_interleave(first, n).to(torch.int32).to(device),
+            "hi": torch.repeat_interleave(end, n).to(torch.int32).to(device), "max_len": int(n.max()) if len(n) else 0}
 
 
 class EncoderLayers:
@@ -242,88 +248,132 @@ class EncoderLayers:
         return x
 
 
+def _halve(t: int) -> int:
+    """Length after a 3-tap, stride-2 convolution padded by one on each side."""
+    return (t + 1) // 2
+
+
+class SubsamplingStem:
+    """The encoder's 8x time-subsampling front (transformers ParakeetEncoderSubsamplingConv2D: a 3x3 convolution,
+    then two depthwise + pointwise pairs, ReLU after each pointwise, then a linear to d_model), prepared once for this
+    library's kernels (reference fast_encoder.py:165-200 describes the same operation sequence):
+
+    - sub_conv0_dw fuses the first convolution and the first depthwise one; both take fp32 taps flattened to (C, 9)
+      and fp32 biases;
+    - each pointwise convolution is a bf16 GEMM over rows of (frame, frequency) with channels innermost, its bias
+      added in fp32 before the one rounding, then ReLU (EPI_CONV_RELU);
+    - the final linear reads a frame's (frequency, channel) row; the module flattens (channel, frequency), so its
+      weight columns are permuted here once.
+
+    Every piece is convolved on its own frames only: no padding rows enter the packed output."""
+
+    def __init__(self, sub):
+        convs = [m for m in sub.layers if isinstance(m, torch.nn.Conv2d)]
+        if len(convs) != 5 or convs[1].groups == 1 or convs[2].kernel_size != (1, 1):
+            raise ValueError("SubsamplingStem: expected conv, (depthwise, pointwise) x 2")
+        full, dw1, pw1, dw2, pw2 = convs
+        taps = lambda c: c.weight.detach().float().flatten(1).contiguous()  # noqa: E731
+        vec = lambda t: t.detach().float().contiguous()  # noqa: E731
+        self.first = (taps(full), vec(full.bias), taps(dw1), vec(dw1.bias))
+        self.second_dw = (taps(dw2), vec(dw2.bias))
+        self.pointwise = [(c.weight.detach().flatten(1).contiguous(), c.bias.detach().contiguous()) for c in (pw1, pw2)]
+        self.c = pw2.out_channels
+        self.freq = sub.linear.in_features // self.c
+        lin_w = sub.linear.weight.detach().unflatten(1, (self.c, self.freq)).transpose(1, 2).flatten(1)
+        self.linear = (lin_w.contiguous(), sub.linear.bias.detach().contiguous())
+
+    @staticmethod
+    def lengths(frames: list[int]) -> tuple[list[int], list[int]]:
+        """Per piece, its length after the fused first stage (stride 4) and after the whole stem (stride 8)."""
+        quarter = [_halve(_halve(f)) for f in frames]
+        return quarter, [_halve(t) for t in quarter]
+
+    @staticmethod
+    def _row_index(counts: list[int], dev) -> torch.Tensor:
+        """int32 (sum(counts), 2): (piece, row within the piece) for every output row of a stage."""
+        c = torch.tensor(counts, dtype=torch.int64)
+        piece = torch.repeat_interleave(torch.arange(len(c)), c)
+        within = torch.arange(int(c.sum())) - torch.repeat_interleave(c.cumsum(0) - c, c)
+        return torch.stack([piece, within], 1).to(torch.int32).to(dev, non_blocking=True)
+
+    @torch.no_grad()
+    def __call__(self, features: torch.Tensor, frames: list[int]) -> tuple[torch.Tensor, list[int]]:
+        dev, dt, C = features.device, features.dtype, self.c
+        quarter, eighth = self.lengths(frames)
+        as_dev = lambda v: torch.tensor(v, dtype=torch.int32).to(dev, non_blocking=True)  # noqa: E731
+        # stage 1: (rows at stride 4, 32 frequencies, C) from the log-mel frames of each piece
+        h = torch.empty(sum(quarter), 32, C, device=dev, dtype=dt)
+        ext.sub_conv0_dw(features.contiguous(), as_dev(frames), self._row_index(quarter, dev), *self.first, h)
+        h = gemm(h.view(-1, C), *self.pointwise[0], EPI_CONV_RELU).view(-1, 32, C)
+        # stage 2: depthwise at stride 2 in time and frequency, within each piece's rows of stage 1
+        first_row = [0]
+        for t in quarter[:-1]:
+            first_row.append(first_row[-1] + t)
+        g = torch.empty(sum(eighth), 16, C, device=dev, dtype=dt)
+        ext.sub_dw(h, as_dev(first_row), as_dev(quarter), self._row_index(eighth, dev), *self.second_dw, g)
+        g = gemm(g.view(-1, C), *self.pointwise[1], EPI_CONV_RELU)
+        return gemm(g.view(-1, self.freq * C), *self.linear, EPI_BIAS), eighth
+
+
+def load_pruned_feed_forwards(encoder, path: str) -> None:
+    """Put a file of 2:4-pruned feed-forward second-layer weights into the module (the format kernels/sparse.py
+    writes, reference sparse.py:86-120: {"<layer>.feed_forward<1|2>": weight}). Every layer's two feed-forwards must
+    be present with the module's shapes; nothing is changed otherwise."""
+    state = torch.load(path, weights_only=True)
+    targets = {f"{i}.{ff}": getattr(blk, ff).linear2.weight
+               for i, blk in enumerate(encoder.layers) for ff in ("feed_forward1", "feed_forward2")}
+    if set(state) != set(targets):
+        raise ValueError(f"FastEncoder: {path} must hold exactly {len(targets)} entries <layer>.feed_forward<1|2>")
+    bad = [k for k, w in state.items() if w.shape != targets[k].shape]
+    if bad:
+        raise ValueError(f"FastEncoder: wrong shapes for {bad}")
+    with torch.no_grad():
+        for k, w in state.items():
+            targets[k].copy_(w)
+
+
 class FastEncoder:
-    """A transformers ParakeetEncoder (bf16, on the GPU) on packed pieces (reference fast_encoder.py:133-232): the
-    subsampling stem per piece without padding (sub_conv0_dw, the pointwise convolutions and final linear as bf16
-    GEMMs, sub_dw), then the native layer loop: W8A8 with int8, else bf16 (the reference's default). sparse (int8
-    only): a file of 2:4-pruned second feed-forward weights (as the reference), or True to prune them by magnitude
-    here; None keeps every layer dense. sparse_w1 prunes the feed-forwards' first linears 2:4 by magnitude as well
-    (this build's option: every feed-forward linear 2:4)."""
+    """A transformers ParakeetEncoder (1280 wide, bf16 on the GPU) over packed pieces: SubsamplingStem, then the
+    native layer loop (EncoderLayers), W8A8 with int8 or bf16 without (the reference's FastEncoder surface,
+    fast_encoder.py:133-232: the constructor arguments, subsample / metadata / layers_forward / __call__).
+
+    sparse needs int8: a path to a pruned-weights file (load_pruned_feed_forwards), or True to prune the
+    feed-forwards' second linears 2:4 by magnitude at conversion; None / False keeps them dense. sparse_w1 prunes the
+    feed-forwards' first linears as well (not in the reference)."""
 
     MAX_LEN = MAX_LEN
 
     def __init__(self, encoder, int8: bool = False, sparse: str | bool | None = None, sparse_w1: bool = False):
-        if (sparse is not None and sparse is not False or sparse_w1) and not int8:
+        wants_24 = sparse_w1 or (sparse is not None and sparse is not False)
+        if wants_24 and not int8:
             raise ValueError("FastEncoder: the 2:4 feed-forwards need int8")
-        cfg = encoder.config
-        if cfg.hidden_size != 1280 or getattr(cfg, "scale_input", False):
+        if encoder.config.hidden_size != 1280 or getattr(encoder.config, "scale_input", False):
             raise ValueError("FastEncoder: 1280-wide encoders without input scaling only")
         if isinstance(sparse, str):
-            pruned = torch.load(sparse, weights_only=True)
-            with torch.no_grad():
-                for key, w in pruned.items():
-                    i, name = key.split(".")
-                    lin = getattr(encoder.layers[int(i)], name).linear2
-                    if w.shape != lin.weight.shape:
-                        raise ValueError(f"FastEncoder: {key} has shape {tuple(w.shape)}")
-                    lin.weight.copy_(w.to(lin.weight.device, lin.weight.dtype))
-            if len(pruned) != 2 * len(encoder.layers):
-                raise ValueError("FastEncoder: the file must prune every feed-forward's second layer")
-        self.encoder, self.int8, self.sparse = encoder, int8, sparse is not None and sparse is not False
+            load_pruned_feed_forwards(encoder, sparse)
+        self.encoder, self.int8 = encoder, int8
+        self.sparse = sparse is not None and sparse is not False
+        with torch.no_grad():
+            self.stem = SubsamplingStem(encoder.subsampling)
         self.layers = EncoderLayers(encoder.layers, encoder.encode_positions.inv_freq, sparse=self.sparse,
                                     max_len=self.MAX_LEN, sparse_w1=sparse_w1, int8=int8)
-        with torch.no_grad():
-            # subsampling: [conv0, ReLU, dw, pw, ReLU, dw, pw, ReLU] + linear; the linear's input columns reordered
-            # from (channel, frequency) to the channels-last (frequency, channel)
-            sub = encoder.subsampling
-            conv0, dw2, pw3, dw5, pw6 = (sub.layers[i] for i in (0, 2, 3, 5, 6))
-            f32 = lambda t: t.float().reshape(t.shape[0], -1).contiguous()  # noqa: E731
-            self.sub_c0 = (f32(conv0.weight), conv0.bias.float().contiguous(), f32(dw2.weight),
-                           dw2.bias.float().contiguous())
-            self.sub_pw3 = (pw3.weight[:, :, 0, 0].contiguous(), pw3.bias.contiguous())
-            self.sub_dw5 = (f32(dw5.weight), dw5.bias.float().contiguous())
-            self.sub_pw6 = (pw6.weight[:, :, 0, 0].contiguous(), pw6.bias.contiguous())
-            ch, out_f = pw6.out_channels, sub.linear.in_features // pw6.out_channels
-            self.sub_lin = (sub.linear.weight.view(-1, ch, out_f).transpose(1, 2).reshape(-1, ch * out_f).contiguous(),
-                            sub.linear.bias.contiguous())
-        self.channels = ch
 
-    @torch.no_grad()
     def subsample(self, features: torch.Tensor, frames: list[int]) -> tuple[torch.Tensor, list[int]]:
-        """Each piece's first frames[i] log-mel frames of the padded batch features (B, T, 128) through the
-        subsampling convolutions, on its own (no padding), channels-last: packed (N, 1280) and the lengths."""
-        dev, C = features.device, self.channels
-        half = lambda n: [(t - 1) // 2 + 1 for t in n]  # noqa: E731  3x3, stride 2, padding 1
-        t2 = half(half(frames))
-        t3 = half(t2)
-        rows = lambda ts: torch.tensor([(i, t) for i, n in enumerate(ts) for t in range(n)],  # noqa: E731
-                                       dtype=torch.int32).reshape(-1, 2).to(dev, non_blocking=True)
-        i32 = lambda v: torch.tensor(v, dtype=torch.int32).to(dev, non_blocking=True)  # noqa: E731
-        n2, n3 = sum(t2), sum(t3)
-        a2 = torch.empty(n2, 32, C, device=dev, dtype=features.dtype)
-        ext.sub_conv0_dw(features.contiguous(), i32(frames), rows(t2), *self.sub_c0, a2)
-        a3 = gemm(a2.view(n2 * 32, C), *self.sub_pw3, EPI_CONV_RELU)
-        a5 = torch.empty(n3, 16, C, device=dev, dtype=features.dtype)
-        starts = [sum(t2[:i]) for i in range(len(t2))]
-        ext.sub_dw(a3.view(n2, 32, C), i32(starts), i32(t2), rows(t3), *self.sub_dw5, a5)
-        a6 = gemm(a5.view(n3 * 16, C), *self.sub_pw6, EPI_CONV_RELU)
-        return gemm(a6.view(n3, 16 * C), *self.sub_lin, EPI_BIAS), t3
+        """features: padded log-mel (B, T, 128); piece b uses its first frames[b] frames. Returns the packed stem
+        output (sum of lengths, 1280) and the per-piece lengths."""
+        return self.stem(features, frames)
 
     def metadata(self, lengths: list[int], device) -> dict:
         return metadata(lengths, device)
 
-    @torch.no_grad()
     def layers_forward(self, x: torch.Tensor, meta: dict) -> torch.Tensor:
-        """Every layer on packed frames x (N, 1280), in place (the native loop); returns x."""
+        """All layers over the packed rows x in place; returns x."""
         return self.layers(x, None, meta)
 
-    @torch.no_grad()
     def __call__(self, features: torch.Tensor, frames: list[int]) -> tuple[torch.Tensor, list[int]]:
-        """Packed hidden states (sum of lengths, 1280) and the lengths of the pieces whose first frames[i] frames are
-        in the padded batch features (B, T, 128)."""
         x, lengths = self.subsample(features, frames)
-        return self.layers_forward(x, self.metadata(lengths, x.device)), lengths
+        return self.layers_forward(x, metadata(lengths, x.device)), lengths
 
 
-__all__ = ["EncoderLayer", "FastEncoder", "gemm", "EncoderLayers", "LAYER_FIELDS", "metadata", "relative_table", "EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
+__all__ = ["EncoderLayer", "FastEncoder", "SubsamplingStem", "load_pruned_feed_forwards", "gemm", "EncoderLayers", "LAYER_FIELDS", "metadata", "relative_table", "EPI_BIAS", "EPI_GLU", "EPI_RESID", "EPI_SILU_Q8", "I8_CFG", "I8_CFG_GROUPED", "I8_CFG_FF1", "FF_GROUP",
            "I8_SMALL", "SP_CONFIGS", "Int8Linear", "i8_config", "quantize_activations", "quantize_rows"]

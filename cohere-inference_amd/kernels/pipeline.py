@@ -152,6 +152,9 @@ class Pipeline:
     CHUNK_FRAMES = 3000  # encoder frames per encoder call (reference pipeline.py:61)
     LAG = 1  # steps between a step's launch and the host reading its end flags (reference pipeline.py:64)
     MAX_WAIT_S = 0.75  # a piece waiting longer than this goes first in the next chunk, whatever its length
+    # the order of the pieces that have not waited that long: "short_then_long" takes the shortest third first (early
+    # answers for short requests), then the rest longest first (a short decoding tail); "short" shortest first
+    ORDER = "short_then_long"
 
     def __init__(self, model, extractor=None, slots: int = 128, max_new_tokens: int = 448, int8: bool = False,
                  sparse: str | bool | None = None, *, frames: int | None = None, buckets=None,
@@ -238,6 +241,7 @@ class Pipeline:
         """Decode dithered pieces (prepare()) with this prompt; the future's result is one int64 array per piece,
         prompt + generated ids. max_new: tokens to generate at most per piece (default the decoder's max_new_tokens).
         The samples are copied to the GPU here, on a stream of their own."""
+        self._validate(pieces, prompt)
         req = _Request(len(pieces))
         if not pieces:
             req.future.set_result([])
@@ -255,6 +259,19 @@ class Pipeline:
                 self._waiting.append(_Piece(x, prompt, max_new[k] if max_new else None, req, k, ready))
             self._cv.notify_all()
         return req.future
+
+    def _validate(self, pieces: list, prompt: torch.Tensor) -> None:
+        """Raise ValueError in the caller for what the decoder would refuse at admission: a prompt outside
+        1..max_prompt tokens, or a piece longer than the encoder frames a slot holds (samples // 1280 + 1 is the exact
+        encoder length: a centred 160-sample hop, then three stride-2 halvings)."""
+        dec = self.decoder
+        if not 1 <= len(prompt) <= dec.max_prompt:
+            raise ValueError(f"Pipeline: a prompt of {len(prompt)} tokens (1..{dec.max_prompt})")
+        for x in pieces:
+            frames = len(x) // 1280 + 1
+            if frames > dec.frames:
+                raise ValueError(f"Pipeline: a piece of {len(x)} samples needs {frames} encoder frames "
+                                 f"(at most {dec.frames})")
 
     def close(self) -> None:
         """Stop the service threads once the work they hold is done (pending requests are answered first)."""
@@ -277,12 +294,15 @@ class Pipeline:
 
     def _next_chunk(self) -> tuple[list[_Piece], list[int]]:
         """(lock held) The next chunk and its slots: pieces that have waited longer than MAX_WAIT_S first, in
-        arrival order, then the rest shortest first (early answers for short requests)."""
+        arrival order, then the rest in ORDER (reference pipeline.py:120-131)."""
         if not self._waiting or not self._free:
             return [], []
         now = time.perf_counter()
         late = [p for p in self._waiting if now - p.arrived > self.MAX_WAIT_S]
         rest = sorted((p for p in self._waiting if now - p.arrived <= self.MAX_WAIT_S), key=lambda p: p.n)
+        if self.ORDER == "short_then_long" and len(rest) > 8:
+            third = len(rest) // 3
+            rest = rest[:third] + rest[third:][::-1]
         chunk = self._chunk(late + rest, len(self._free))
         taken = {id(p) for p in chunk}
         self._waiting = [p for p in self._waiting if id(p) not in taken]
@@ -331,19 +351,37 @@ class Pipeline:
                 new = list(self._encoded)
                 self._encoded.clear()
             for slots, chunk, lengths in new:
-                run.admit(slots, chunk, lengths)
-            if run.active:
-                run.step()
-                self.stats["steps"] += 1
-            ended = run.harvest()
-            if not run.active:
-                run.drain()
+                try:
+                    run.admit(slots, chunk, lengths)
+                except Exception as exc:  # noqa: BLE001 -- the chunk's requests fail, its slots are freed
+                    self._release(slots, chunk, exc)
+            try:
+                if run.active:
+                    run.step()
+                    self.stats["steps"] += 1
+                ended = run.harvest()
+                if not run.active:
+                    run.drain()
+            except Exception as exc:  # noqa: BLE001 -- every piece being decoded fails; the service goes on
+                held = [(s, run.holder[s]) for s in run.active if s in run.holder]
+                self._release([s for s, _ in held], [p for _, p in held], exc)
+                run = _Decoding(self.decoder, self.LAG)
+                continue
             for _, p in ended:
                 p.request.deliver(p.k, p.tokens)
             if ended:
                 with self._cv:
                     self._free.extend(s for s, _ in ended)
                     self._cv.notify_all()
+
+    def _release(self, slots: list[int], pieces: list[_Piece], exc: BaseException) -> None:
+        """Fail the pieces' requests and return their slots."""
+        for p in pieces:
+            if p.request is not None:
+                p.request.fail(exc)
+        with self._cv:
+            self._free.extend(slots)
+            self._cv.notify_all()
 
 
 __all__ = ["Pipeline"]

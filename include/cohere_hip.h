@@ -173,10 +173,11 @@ int cohere_dec_add_ln(uint16_t* x, const uint16_t* y, int64_t ldy, const uint16_
  * self != 0: q is the qkv projection [rows, ldq] (q | k | v, heads x 128 each), the new key and value are first
  * written into the caches at position n[s] and attended as computed, with keys 0 .. n[s]-1 from the cache; self == 0:
  * q [rows, ldq] over the slot's n[s] audio frames. Caches k, v bf16 (slots, heads, T, 128). splits > 1 splits each
- * (row, head)'s keys over workgroups and needs part with rows x heads x splits x 130 floats. The kernels address a
- * cache with 32-bit element offsets: slots x heads x T x 128 must stay below 2^32. */
+ * (row, head)'s keys over workgroups and needs part with rows x heads x splits x 130 floats. slots is the caches'
+ * first dimension: the kernels address a cache with 32-bit element offsets, so slots x heads x T x 128 must stay
+ * below 2^32 (refused otherwise). */
 int cohere_dec_attention(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
-                         uint16_t* k, uint16_t* v, const int32_t* n, int64_t heads, int64_t T, float scale,
+                         uint16_t* k, uint16_t* v, const int32_t* n, int64_t slots, int64_t heads, int64_t T, float scale,
                          int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream);
 
 /* Replaces dec_attention_q8 (reference kernels/csrc/decoder_ops.cu:264-290, bound at kernels/csrc/bindings.cpp:81):
@@ -184,7 +185,7 @@ int cohere_dec_attention(int32_t self, const int32_t* active, int64_t rows, cons
  * one per 128-vector; self-attention writes the new key and value quantized (absmax / 127, round half even) and
  * attends to them unquantized. */
 int cohere_dec_attention_q8(int32_t self, const int32_t* active, int64_t rows, const uint16_t* q, int64_t ldq,
-                            int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n, int64_t heads, int64_t T,
+                            int8_t* k8, int8_t* v8, float* ks, float* vs, const int32_t* n, int64_t slots, int64_t heads, int64_t T,
                             float scale, int64_t splits, float* part, int64_t part_len, uint16_t* out, void* stream);
 
 /* Replaces dec_pick (reference kernels/csrc/decoder_ops.cu:106-159, 304-314, bound at kernels/csrc/bindings.cpp:83):

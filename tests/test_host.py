@@ -89,6 +89,13 @@ def test_c_abi_rejects_bad_arguments_without_launching():
     assert rc != 0 and "multiple of 64" in msg
     rc, msg = _raw(lib, "cohere_sub_dw", fake, fake, fake, fake, 3, fake, fake, fake, 32, 12, None)
     assert rc != 0 and "C % 8" in msg
+    # decoder attention: caches of 2^32 elements or more (the kernels' offsets are 32-bit)
+    rc, msg = _raw(lib, "cohere_dec_attention_q8", 1, fake, 64, fake, 3072, fake, fake, fake, fake, fake, 1 << 16, 8,
+                   512, 0.1, 1, None, 0, fake, None)
+    assert rc != 0 and "2^32" in msg
+    rc, msg = _raw(lib, "cohere_dec_attention", 0, fake, 64, fake, 1024, fake, fake, fake, 0, 8, 512, 0.1, 1, None,
+                   0, fake, None)
+    assert rc != 0 and "2^32" in msg
     assert _raw(lib, "cohere_logmel_features", None, None, 0, 0, None, None, None, 0.97, None, 0, None, None)[0] == 0
     assert lib.cohere_logmel_workspace_bytes(100) == 100 * 128 * 4
 

@@ -1,7 +1,8 @@
 """Host-side scheduling of the pipeline service (no GPU): how the encoder thread cuts chunks from the waiting pieces
 (reference kernels/pipeline.py:144-183 -- as many pieces as there are free slots, within CHUNK_FRAMES encoder frames,
 at least one piece) and in which order it takes them (pieces that waited longer than MAX_WAIT_S first, in arrival
-order, then the rest shortest first), and how a request's future completes."""
+order, then the rest in ORDER: the shortest third, then the others longest first), how submit() refuses what the
+decoder would refuse, and how a request's future completes."""
 
 from __future__ import annotations
 
@@ -19,8 +20,8 @@ def _piece(n: int, arrived: float = 0.0) -> _Piece:
     return p
 
 
-def _stub(chunk_frames=3000, waiting=(), free=(), max_wait=0.75):
-    st = types.SimpleNamespace(CHUNK_FRAMES=chunk_frames, MAX_WAIT_S=max_wait, _waiting=list(waiting),
+def _stub(chunk_frames=3000, waiting=(), free=(), max_wait=0.75, order="short_then_long"):
+    st = types.SimpleNamespace(CHUNK_FRAMES=chunk_frames, MAX_WAIT_S=max_wait, ORDER=order, _waiting=list(waiting),
                                _free=list(free))
     st._chunk = lambda queue, room: Pipeline._chunk(st, queue, room)
     return st
@@ -56,6 +57,39 @@ def test_next_chunk_order_late_first_then_shortest(monkeypatch):
     assert chunk == [late_long, late_short, fresh_short, fresh_long]
     assert slots == [3, 4, 5, 6] and st._free == [7]
     assert st._waiting == []
+
+
+def test_next_chunk_short_then_long_over_eight(monkeypatch):
+    """With more than 8 fresh pieces: the shortest third first, then the remaining ones longest first (reference
+    pipeline.py:126-128); with 8 or fewer, or ORDER "short", plain shortest first."""
+    import kernels.pipeline as pl
+
+    monkeypatch.setattr(pl.time, "perf_counter", lambda: 0.0)
+    ps = [_piece(1280 * (10 * i + 9)) for i in (3, 7, 0, 9, 1, 5, 8, 2, 6, 4, 10)]  # 11 fresh pieces, shuffled
+    by_len = sorted(ps, key=lambda p: p.n)
+    st = _stub(waiting=ps, free=list(range(20)))
+    chunk, _ = Pipeline._next_chunk(st)
+    assert chunk == by_len[:3] + by_len[3:][::-1]
+    st = _stub(waiting=ps, free=list(range(20)), order="short")
+    assert Pipeline._next_chunk(st)[0] == by_len
+    st = _stub(waiting=ps[:8], free=list(range(20)))
+    assert Pipeline._next_chunk(st)[0] == sorted(ps[:8], key=lambda p: p.n)
+
+
+def test_submit_validates_in_the_caller():
+    """A prompt outside 1..max_prompt or a piece beyond the slot's encoder frames raises ValueError in submit()
+    (before any thread starts), instead of killing the decoder thread at admission."""
+    import torch
+
+    st = types.SimpleNamespace(decoder=types.SimpleNamespace(max_prompt=4, frames=376))
+    ok = np.zeros(480000, np.float32)  # 376 frames
+    Pipeline._validate(st, [ok], torch.tensor([1, 2]))
+    with pytest.raises(ValueError, match="prompt"):
+        Pipeline._validate(st, [ok], torch.tensor([], dtype=torch.long))
+    with pytest.raises(ValueError, match="prompt"):
+        Pipeline._validate(st, [ok], torch.arange(5))
+    with pytest.raises(ValueError, match="encoder frames"):
+        Pipeline._validate(st, [ok, np.zeros(480000 + 1280, np.float32)], torch.tensor([1]))
 
 
 def test_next_chunk_bounded_by_free_slots_and_frames(monkeypatch):
