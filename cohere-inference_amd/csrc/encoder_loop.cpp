@@ -214,10 +214,9 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
     const void* const* ly = fields + l * N_FIELDS;
     for (int f : required)
       COHERE_REQUIRE(ly[f], "encoder_layers: layer " + std::to_string(l) + " misses field " + std::to_string(f));
-    COHERE_REQUIRE((ly[SP_FF1_W] ? ly[SP_FF1_E] != nullptr : ly[Q_FF1_W2] != nullptr) &&
-                       (ly[SP_FF2_W] ? ly[SP_FF2_E] != nullptr : ly[Q_FF2_W2] != nullptr) &&
-                       (ly[SP_FF1_W1] ? ly[SP_FF1_E1] != nullptr : ly[Q_FF1_W1] != nullptr) &&
-                       (ly[SP_FF2_W1] ? ly[SP_FF2_E1] != nullptr : ly[Q_FF2_W1] != nullptr),
+    // a 2:4 weight without selectors is in the stage-tiled layout (cohere_pack_24_tiled)
+    COHERE_REQUIRE((ly[SP_FF1_W] || ly[Q_FF1_W2]) && (ly[SP_FF2_W] || ly[Q_FF2_W2]) &&
+                       (ly[SP_FF1_W1] || ly[Q_FF1_W1]) && (ly[SP_FF2_W1] || ly[Q_FF2_W1]),
                    "encoder_layers: layer " + std::to_string(l) +
                        ": a feed-forward linear has neither dense nor 2:4 weights");
   }
@@ -244,7 +243,12 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
   }(), "encoder_layers: a 2:4 first feed-forward linear needs the feed-forward group 256");
   auto ffn = [&](const void* const* ly, int w1, int s1, int b1, int w2, int s2, int b2, int spw, int spe, int spw1,
                  int spe1) {
-    if (ly[spw1]) {
+    if (ly[spw1] && !ly[spe1]) {
+      RUN(cohere_gemm_sp_tiled(ws.hq, DM, ws.hs, 1, DM, fld<uint8_t>(ly, spw1), fld<float>(ly, s1),
+                               fld<uint16_t>(ly, b1), ws.tq, DFF, COHERE_EPI_SILU_Q8, nullptr, 0, 1.f, ws.ts, ts_ld,
+                               rows, DFF, DM, (int32_t)c_sp, stream),
+          "feed-forward W1 (2:4, tiled)");
+    } else if (ly[spw1]) {
       RUN(cohere_gemm_sp(ws.hq, DM, ws.hs, 1, DM, fld<int8_t>(ly, spw1), fld<int32_t>(ly, spe1), fld<float>(ly, s1),
                          fld<uint16_t>(ly, b1), ws.tq, DFF, COHERE_EPI_SILU_Q8, nullptr, 0, 1.f, ws.ts, ts_ld, rows,
                          DFF, DM, (int32_t)c_sp, stream),
@@ -255,7 +259,12 @@ extern "C" int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* cons
                          (int32_t)c_ff1, stream),
           "feed-forward W1");
     }
-    if (ly[spw]) {
+    if (ly[spw] && !ly[spe]) {
+      RUN(cohere_gemm_sp_tiled(ws.tq, DFF, ws.ts, ts_ld, group, fld<uint8_t>(ly, spw), fld<float>(ly, s2),
+                               fld<uint16_t>(ly, b2), x, DM, COHERE_EPI_RESID, x, DM, 0.5f, nullptr, 0, rows, DM, DFF,
+                               (int32_t)c_sp, stream),
+          "feed-forward W2 (2:4, tiled)");
+    } else if (ly[spw]) {
       RUN(cohere_gemm_sp(ws.tq, DFF, ws.ts, ts_ld, group, fld<int8_t>(ly, spw), fld<int32_t>(ly, spe),
                          fld<float>(ly, s2), fld<uint16_t>(ly, b2), x, DM, COHERE_EPI_RESID, x, DM, 0.5f, nullptr, 0,
                          rows, DM, DFF, (int32_t)c_sp, stream),

@@ -63,7 +63,17 @@ struct GemmArgs {
   float alpha;
   int xcd_rows;          // > 0: the token tiles split into xcd_rows parts and the channel tiles into 8 / xcd_rows,
                          // one part each per XCD (set by launch_tile); 0: contiguous tile ranges per XCD
+  int tiled;             // 2:4 only: W holds the stage-tiled layout of the kept values and selectors (E unused)
 };
+
+// The stage-tiled 2:4 weight layout (cohere_pack_24_tiled): for each block of 16 output channels rb and each
+// 128-wide K stage kt, one contiguous record of TILED_REC bytes at (rb * K/128 + kt) * TILED_REC: 1024 bytes of kept
+// values, 16-byte chunk i holding row i / 4's logical chunk (i % 4) ^ ((i / 8) % 4) of its 64 kept bytes of the stage
+// (the LDS swizzle, so a DMA lane's 16 bytes land where the fragment reads expect them), then 256 bytes of
+// selectors, row r's four words of the stage at 16 r. Every 1 KB DMA instruction then reads one contiguous kilobyte
+// (row-major weights give 16 rows x 64 bytes: half of each 128-byte line), and a stage's selectors of 16 rows one
+// 256-byte run (row-major: 16 bytes of each of 16 lines).
+constexpr int TILED_REC = 1280;
 
 constexpr int LDS_BYTES = 160 * 1024;
 inline bool g_xcd_split = true;  // tuning hook (cohere_set_gemm_tile with tile -2 / -3 switches it)
@@ -257,6 +267,18 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
         if (half) lc &= 3;
         dma16(p.W + (int64_t)(n0 + r) * K + k0 + lc * 16, wbase + s * 1024);
       }
+    } else if (p.tiled) {
+      // stage-tiled weights: instruction s takes the kept values of channel block (n0 / 16 + s), stage kt
+      const int8_t* rec = p.W + ((int64_t)(n0 >> 4) * KT + kt) * TILED_REC;
+#pragma unroll
+      for (int j = 0; j < T::W_SLOTS / NW; ++j) {
+        const int s = wave + j * NW;
+        dma16(rec + (int64_t)s * KT * TILED_REC + lane * 16, wbase + s * 1024);
+      }
+      constexpr int ER = BN / NW;
+      char* ebase = wbase + T::W_STAGE + wave * ER * 16;
+      const int r = wave * ER + lane;
+      if (lane < ER) dma16(rec + (int64_t)(r >> 4) * KT * TILED_REC + 1024 + (r & 15) * 16, ebase);
     } else {
 #pragma unroll
       for (int j = 0; j < T::W_SLOTS / NW; ++j) {  // kept values: 16 rows of 64 B per instruction

@@ -3,6 +3,7 @@
 #include "cohere_hip.h"
 #include "gemm_q8.h"
 
+#include <cstring>
 #include <string>
 
 namespace {
@@ -142,6 +143,43 @@ extern "C" int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int
   p.ldx = ldx; p.ldsx = ldsx; p.ldc = ldc; p.ldr = ldr; p.ldqs = ldqs;
   p.M = (int)M; p.N = (int)N; p.K = (int)K; p.qgroup = 256; p.epi = epi; p.alpha = alpha;
   return gemm_entry<true>(p, group, 128, reinterpret_cast<hipStream_t>(stream), "gemm_sp");
+}
+
+extern "C" int cohere_gemm_sp_tiled(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, int64_t group,
+                                    const uint8_t* wt, const float* sw, const uint16_t* bias, void* out, int64_t ldc,
+                                    int32_t epi, const uint16_t* resid, int64_t ldr, float alpha, float* qs,
+                                    int64_t ldqs, int64_t M, int64_t N, int64_t K, int32_t cfg, void* stream) {
+  cohere::clear_error();
+  COHERE_REQUIRE(cfg >= -1 && cfg <= 4, "gemm_sp_tiled: unknown config " + std::to_string(cfg));
+  GemmArgs p{};
+  p.X = x; p.sx = sx; p.W = reinterpret_cast<const int8_t*>(wt); p.E = reinterpret_cast<const int32_t*>(wt);
+  p.sw = sw; p.bias = bias; p.C = out; p.R = resid; p.qs = qs; p.tiled = 1;
+  p.ldx = ldx; p.ldsx = ldsx; p.ldc = ldc; p.ldr = ldr; p.ldqs = ldqs;
+  p.M = (int)M; p.N = (int)N; p.K = (int)K; p.qgroup = 256; p.epi = epi; p.alpha = alpha;
+  return gemm_entry<true>(p, group, 128, reinterpret_cast<hipStream_t>(stream), "gemm_sp_tiled");
+}
+
+extern "C" int64_t cohere_pack_24_tiled_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0 || N % 16 || K % 128) return -1;
+  return N / 16 * (K / 128) * TILED_REC;
+}
+
+extern "C" int cohere_pack_24_tiled(const int8_t* wc, const int32_t* e, int64_t N, int64_t K, uint8_t* out) {
+  cohere::clear_error();
+  COHERE_REQUIRE(wc && e && out, "pack_24_tiled: null pointer");
+  COHERE_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 128 == 0, "pack_24_tiled: N % 16 and K % 128 must be 0");
+  const int64_t KT = K / 128;
+  for (int64_t rb = 0; rb < N / 16; ++rb)
+    for (int64_t kt = 0; kt < KT; ++kt) {
+      uint8_t* rec = out + (rb * KT + kt) * TILED_REC;
+      for (int i = 0; i < 64; ++i) {
+        const int64_t row = rb * 16 + i / 4;
+        const int c = (i % 4) ^ ((i / 8) % 4);
+        std::memcpy(rec + 16 * i, wc + row * (K / 2) + kt * 64 + c * 16, 16);
+      }
+      for (int r = 0; r < 16; ++r) std::memcpy(rec + 1024 + 16 * r, e + (rb * 16 + r) * (K / 32) + kt * 4, 16);
+    }
+  return 0;
 }
 
 extern "C" int cohere_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* w, const uint16_t* bias, uint16_t* out,

@@ -26,6 +26,7 @@ LIB_PATH = os.environ.get("COHERE_HIP_LIBRARY") or os.path.join(_PKG, "lib", "li
 
 EPI_BIAS, EPI_SILU, EPI_RELU, EPI_RESID, EPI_GLU, EPI_SILU_Q8, EPI_CONV_RELU = range(7)
 DEC_EP_NONE, DEC_EP_RELU, DEC_EP_RESID = range(3)  # dec_linear_fused's epilogues
+TILED_REC = 1280  # bytes per record of the stage-tiled 2:4 weight layout (kernels.sparse.pack_24_tiled)
 EPI_I32 = 7  # raw int32 accumulators: a parity hook with no counterpart in the reference
 
 # every symbol include/cohere_hip.h declares
@@ -36,7 +37,8 @@ EXPORTS = ("cohere_gemm_i8", "cohere_gemm_sp", "cohere_quantize_rows", "cohere_l
            "cohere_dec_add_ln", "cohere_dec_attention", "cohere_dec_attention_q8", "cohere_dec_pick",
            "cohere_dec_scatter_kv", "cohere_dec_scatter_kv_q8", "cohere_gemm_bf16", "cohere_logmel_workspace_bytes",
            "cohere_logmel_features", "cohere_sub_conv0_dw", "cohere_sub_dw", "cohere_encoder_branch_workspace_bytes",
-           "cohere_encoder_layers_noalloc", "cohere_dec_linear_fused", "cohere_dec_pick_embed")
+           "cohere_encoder_layers_noalloc", "cohere_dec_linear_fused", "cohere_dec_pick_embed",
+           "cohere_gemm_sp_tiled", "cohere_pack_24_tiled_bytes", "cohere_pack_24_tiled")
 
 
 def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
@@ -48,6 +50,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     sig = {
         "cohere_gemm_i8": [P, I64, P, I64, I64, P, P, P, P, I64, I32, P, I64, F, P, I64, I64, I64, I64, I32, P],
         "cohere_gemm_sp": [P, I64, P, I64, I64, P, P, P, P, P, I64, I32, P, I64, F, P, I64, I64, I64, I64, I32, P],
+        "cohere_gemm_sp_tiled": [P, I64, P, I64, I64, P, P, P, P, I64, I32, P, I64, F, P, I64, I64, I64, I64, I32, P],
+        "cohere_pack_24_tiled_bytes": [I64, I64],
+        "cohere_pack_24_tiled": [P, P, I64, I64, P],
         "cohere_quantize_rows": [P, I64, P, I64, P, I64, I64, P],
         "cohere_layernorm_q8": [P, I64, P, P, F, P, P, F, P, I64, P, I64, I64, P],
         "cohere_dec_w8_linear": [P, I64, P, P, P, P, I64, I32, I64, I64, P, I64, P, I64, I64, I64, I64, P],
@@ -249,6 +254,27 @@ class _Ext:
                    _ptr(sw), _ptr(bias), _ptr(out), out.stride(0), int(epi), _ptr(resid),
                    resid.stride(0) if resid is not None else 0, float(alpha), _ptr(qs),
                    qs.stride(0) if qs is not None else 0, M, wc.shape[0], K, int(cfg), _stream())
+
+    def gemm_sp_tiled(self, x, sx, group, wt, sw, bias, out, epi, resid, alpha, qs, cfg):
+        """gemm_sp_epi with the weight in the stage-tiled layout of pack_24_tiled (wt uint8 (N/16, K/128, 1280)):
+        the same results bit for bit, each DMA instruction reading one contiguous kilobyte."""
+        _check(x.dtype == torch.int8 and wt.dtype == torch.uint8 and sx.dtype == torch.float32 and
+               sw.dtype == torch.float32, "gemm_sp_tiled: dtypes")
+        _check(x.stride(1) == 1 and wt.is_contiguous() and wt.dim() == 3 and wt.shape[2] == TILED_REC and
+               sx.stride(1) == 1 and out.stride(1) == 1 and (resid is None or resid.stride(1) == 1),
+               "gemm_sp_tiled: strides / layout")
+        M, K = x.shape
+        N = wt.shape[0] * 16
+        _check(wt.shape[1] * 128 == K and group % 128 == 0 and K % group == 0,
+               "gemm_sp_tiled: wt (N/16, K/128, 1280), group a multiple of 128 dividing K")
+        _check(epi != EPI_RESID or resid is not None, "gemm_sp_tiled: residual epilogue needs resid")
+        _check(epi != EPI_SILU_Q8 or (qs is not None and out.dtype == torch.int8), "gemm_sp_tiled: SILU_Q8 needs qs")
+        if M == 0:
+            return
+        self._call("cohere_gemm_sp_tiled", _ptr(x), x.stride(0), _ptr(sx), sx.stride(0), int(group), _ptr(wt),
+                   _ptr(sw), _ptr(bias), _ptr(out), out.stride(0), int(epi), _ptr(resid),
+                   resid.stride(0) if resid is not None else 0, float(alpha), _ptr(qs),
+                   qs.stride(0) if qs is not None else 0, M, N, K, int(cfg), _stream())
 
     # ---- int8 activation producers (bindings.cpp:44-46, 73-75) --------------------------------------------------
 

@@ -16,10 +16,11 @@ kernels of cohere-inference_amd/csrc (int8 GEMMs, attention, depthwise convoluti
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from kernels.cuda_ext import EPI_BIAS, EPI_CONV_RELU, EPI_GLU, EPI_RESID, EPI_SILU_Q8, ext
-from kernels.sparse import compress_24, prune_24_magnitude
+from kernels.sparse import compress_24, pack_24_tiled, prune_24_magnitude
 
 # The reference's int8 config ids (A10 tile choices). They are accepted and checked by the gfx950 GEMMs (each id keeps
 # its meaning for the SILU_Q8 output group: configs 4, 6, 8 have 256-column groups) but the tiles are chosen for gfx950
@@ -31,6 +32,7 @@ I8_SMALL = {"ff1": ((96, 6), (224, 8), (384, 4), (448, 8)),
             "pw1": ((320, 9), (384, 0), (448, 9)),
             "o": ((640, 9), (896, 0), (1056, 9))}
 SP_CONFIGS = ((448, 2), (2048, 0), (1 << 30, 3))
+RCP127 = float(np.float32(1.0) / np.float32(127.0))  # fp32(1 / 127): PyTorch's GPU `tensor / 127` multiplies by it
 
 
 def i8_config(gemm: str, frames: int, default: int) -> int:
@@ -42,9 +44,11 @@ def i8_config(gemm: str, frames: int, default: int) -> int:
 
 def quantize_rows(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Symmetric int8 per output channel: s = max(amax|w|, 1e-12) / 127 (fp32), q = clamp(round_half_even(w / s),
-    +-127). Load-time weight preparation (reference fast_encoder.py:60-63)."""
+    +-127). Load-time weight preparation (reference fast_encoder.py:60-63). The reference runs it on the GPU, where
+    PyTorch divides a tensor by a Python scalar as a multiplication by the scalar's fp32 reciprocal; the scale is
+    computed that way here on any device (RCP127), so CPU and GPU preparation give the reference's bytes."""
     wf = w.float()
-    s = wf.abs().amax(-1).clamp_min(1e-12) / 127
+    s = wf.abs().amax(-1).clamp_min(1e-12) * RCP127
     return torch.round(wf / s[:, None]).clamp(-127, 127).to(torch.int8).contiguous(), s.contiguous()
 
 
@@ -67,17 +71,22 @@ def quantize_activations(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 class Int8Linear:
     """A W8A8 linear layer: int8 weights per output channel, optionally pruned 2:4 (magnitude, before
-    quantization, as the reference prunes before fast_encoder.py:109 quantizes) and stored compressed."""
+    quantization, as the reference prunes before fast_encoder.py:109 quantizes) and stored compressed. tiled (2:4
+    only): the GEMM reads the stage-tiled copy of the compressed weight (pack_24_tiled; same results, contiguous
+    loads); False reads compress_24's row-major storage."""
 
-    def __init__(self, w: torch.Tensor, bias: torch.Tensor | None, sparse: bool = False):
+    def __init__(self, w: torch.Tensor, bias: torch.Tensor | None, sparse: bool = False, tiled: bool = True):
         if sparse:
             w = prune_24_magnitude(w)
         self.q, self.s = quantize_rows(w)
         self.bias = None if bias is None else bias.to(torch.bfloat16).contiguous()
         self.n, self.k = self.q.shape
         self.sparse = sparse
+        self.wt = None
         if sparse:
             self.wc, self.e = compress_24(self.q)
+            if tiled:
+                self.wt = pack_24_tiled(self.wc, self.e)
 
     def __call__(self, xq: torch.Tensor, xs: torch.Tensor, epi: int = EPI_BIAS, group: int | None = None,
                  out: torch.Tensor | None = None, resid: torch.Tensor | None = None, alpha: float = 1.0,
@@ -90,7 +99,9 @@ class Int8Linear:
             else:
                 out = torch.empty(m, self.n // 2 if epi == EPI_GLU else self.n, dtype=torch.bfloat16,
                                   device=xq.device)
-        if self.sparse:
+        if self.wt is not None:
+            ext.gemm_sp_tiled(xq, xs, group, self.wt, self.s, self.bias, out, epi, resid, alpha, qs, cfg)
+        elif self.sparse:
             ext.gemm_sp_epi(xq, xs, group, self.wc, self.e, self.s, self.bias, out, epi, resid, alpha, qs, cfg)
         else:
             ext.gemm_i8(xq, xs, group, self.q, self.s, self.bias, out, epi, resid, alpha, qs, cfg)
@@ -128,12 +139,15 @@ class EncoderLayer:
     linear W8A8 per output channel; with sparse, the feed-forwards' second linears pruned 2:4 by magnitude (a no-op on
     weights that already are) before quantization and stored compressed, their dense form dropped; sparse_w1 does the
     same to the feed-forwards' first linears (both feed-forward linears 2:4; the reference prunes only the second).
-    Without int8 the linears keep their bf16 weights (the reference's INT8=0 layers)."""
+    Without int8 the linears keep their bf16 weights (the reference's INT8=0 layers). tiled: the layer loop reads the
+    2:4 weights from stage-tiled copies (pack_24_tiled; the same results)."""
 
-    def __init__(self, blk, rk: torch.Tensor, sparse: bool = False, sparse_w1: bool = False, int8: bool = True):
+    def __init__(self, blk, rk: torch.Tensor, sparse: bool = False, sparse_w1: bool = False, int8: bool = True,
+                 tiled: bool = True):
         if (sparse or sparse_w1) and not int8:
             raise ValueError("EncoderLayer: the 2:4 linears are int8 only")
         t = {}
+        self.tiled: dict[str, torch.Tensor] = {}  # stage-tiled copies of the 2:4 weights (pack_24_tiled), by field
         lns = (blk.norm_feed_forward1, blk.norm_self_att, blk.norm_conv, blk.norm_feed_forward2, blk.norm_out)
         self.eps = []
         for name, m in zip(("ff1", "att", "conv", "ff2", "out"), lns):
@@ -186,13 +200,19 @@ class EncoderLayer:
             if pruned:
                 t[q[2]], t[q[3]] = compress_24(t[q[0]])
                 t[q[0]] = none_i8
+                if tiled:
+                    self.tiled[q[2]] = pack_24_tiled(t[q[2]], t[q[3]])
         self.tensors = t
         self.int8 = int8
         self.heads, self.head_dim = at.bias_u.shape
 
     def fields(self) -> list[torch.Tensor]:
-        """This layer's tensors in the reference's field order."""
-        return [self.tensors[k] for k in LAYER_FIELDS]
+        """This layer's tensors in the reference's field order. A 2:4 linear with a stage-tiled copy is passed as that
+        copy in the kept-values field and an empty selectors field (the layer loop then runs gemm_sp_tiled)."""
+        empty = torch.empty(0, device=self.tensors["rk"].device, dtype=torch.int32)
+        sel_of = {"sp_ff1_w": "sp_ff1_e", "sp_ff2_w": "sp_ff2_e", "sp_ff1_w1": "sp_ff1_e1", "sp_ff2_w1": "sp_ff2_e1"}
+        dropped = {sel_of[k] for k in self.tiled}
+        return [self.tiled.get(k, empty if k in dropped else self.tensors[k]) for k in LAYER_FIELDS]
 
 
 def metadata(lengths: list[int], device) -> dict:

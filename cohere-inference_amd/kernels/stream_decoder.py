@@ -18,6 +18,7 @@ from __future__ import annotations
 import torch
 
 from kernels.cuda_ext import DEC_EP_NONE, DEC_EP_RELU, DEC_EP_RESID, ext
+from kernels.fast_encoder import RCP127
 
 # (N, K) -> {rows up to: (columns per CTA, K splits)}: the reference's A10 table, accepted for compatibility. The gfx950
 # kernel checks these like the reference does and then chooses its own tiling (results never depend on it).
@@ -35,11 +36,13 @@ W8_PERM = (0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15)
 
 def prepare_w8(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """bf16 (N, K) -> (uint8 (N, K) = int8 + 128 with K permuted within every 16 by W8_PERM, fp32 per-channel
-    scales). Quantization: s = max(amax|w|, 1e-12) / 127, q = clamp(round_half_even(w / s), +-127)."""
+    scales). Quantization: s = max(amax|w|, 1e-12) / 127, q = clamp(round_half_even(w / s), +-127), the scale's
+    division by 127 as the reference's GPU execution of it: a multiplication by fp32(1 / 127) (RCP127, see
+    kernels.fast_encoder.quantize_rows), on any device."""
     n, k = w.shape
     assert k % 16 == 0
     wf = w.float()
-    s = wf.abs().amax(1).clamp_min(1e-12) / 127
+    s = wf.abs().amax(1).clamp_min(1e-12) * RCP127
     q = (torch.round(wf / s[:, None]).clamp(-127, 127) + 128).to(torch.uint8)
     perm = torch.tensor(W8_PERM, device=w.device)
     return q.reshape(n, k // 16, 16).index_select(2, perm).reshape(n, k).contiguous(), s.contiguous()

@@ -64,6 +64,23 @@ int cohere_gemm_sp(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, 
                    const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M, int64_t N,
                    int64_t K, int32_t cfg, void* stream);
 
+/* No single counterpart in the reference; the same operation as cohere_gemm_sp (reference
+ * kernels/csrc/gemm_sparse.cu:214-253, kernels/sparse.py:26-39 for the weight format) with the 2:4 weight in this
+ * library's stage-tiled layout wt (cohere_pack_24_tiled of the compressed values and selectors): every DMA
+ * instruction then reads one contiguous kilobyte. Same arguments, requirements and results, bit for bit. */
+int cohere_gemm_sp_tiled(const int8_t* x, int64_t ldx, const float* sx, int64_t ldsx, int64_t group, const uint8_t* wt,
+                         const float* sw, const uint16_t* bias, void* out, int64_t ldc, int32_t epi,
+                         const uint16_t* resid, int64_t ldr, float alpha, float* qs, int64_t ldqs, int64_t M,
+                         int64_t N, int64_t K, int32_t cfg, void* stream);
+
+/* Load-time weight preparation for cohere_gemm_sp_tiled (host memory, plain loops; no counterpart in the reference):
+ * compress_24's kept values wc int8 [N, K/2] and selectors e int32 [N, K/32] into out, cohere_pack_24_tiled_bytes(N, K)
+ * bytes (-1 unless N % 16 == 0 and K % 128 == 0). For each block of 16 channels and each 128-wide K stage, one
+ * 1280-byte record: 64 chunks of 16 kept bytes (chunk i = row i/4's chunk (i%4) ^ ((i/8)%4) of the stage), then the
+ * 16 rows' four selector words of the stage. */
+int64_t cohere_pack_24_tiled_bytes(int64_t N, int64_t K);
+int cohere_pack_24_tiled(const int8_t* wc, const int32_t* e, int64_t N, int64_t K, uint8_t* out);
+
 /* Replaces gemm (reference kernels/csrc/gemm.cu:246-279, bound at kernels/csrc/bindings.cpp:65): bf16
  * out = epi(a w^T + bias), a bf16 [M, K] (lda), w bf16 [N, K] contiguous, fp32 accumulation, bias bf16 [N] or
  * null added in fp32 before the first rounding. epi: EPI_BIAS, EPI_SILU (silu(bf16(v))), EPI_RELU, EPI_RESID
@@ -242,7 +259,10 @@ int64_t cohere_encoder_branch_workspace_bytes(int64_t rows, int64_t group, int32
  * kernels/csrc/bindings.cpp:66): every layer of the FastConformer encoder on packed frames x [rows, 1280] bf16, in
  * place, in the reference's launch order. fields: n_layers x COHERE_ENC_N_FIELDS device pointers in the reference's
  * field order, then the 4 extra 2:4 first-linear fields (NULL for the empty tensors: a dense W1 or W2 whose 2:4 form
- * is given, the 2:4 fields of a dense linear, absent biases). eps: n_layers x 5 (ff1, att, conv, ff2, out). tiles / lo / hi / rel_off / max_len / scale as in
+ * is given, the 2:4 fields of a dense linear, absent biases). A 2:4 linear whose kept-values field is set and whose
+ * selectors field is NULL holds its weight in the stage-tiled layout of cohere_pack_24_tiled there (run by
+ * cohere_gemm_sp_tiled; the same results). eps: n_layers x 5 (ff1, att, conv, ff2, out). tiles / lo / hi / rel_off /
+ * max_len / scale as in
  * cohere_relpos_attention and cohere_dwconv_bn_silu; rel_rows the table rows. cfg: the reference's list (bf16 config,
  * int8 QKV, grouped FF W2, FF W1, FF group, PW1, O/PW2, 2:4 FF W2). int8 nonzero runs the W8A8 branch on the
  * quantized fields; int8 zero the bf16 branch (reference encoder_loop.cpp:101-124) on the bf16 weight fields with
@@ -259,7 +279,9 @@ int cohere_encoder_layers(uint16_t* x, int64_t rows, const void* const* fields, 
  * workspace. The loop's buffers live in a file-scope device array of COHERE_ENC_NOALLOC_BYTES (64 MiB) per GPU, held
  * until the process ends; a call whose branch needs more (cohere_encoder_branch_workspace_bytes: above ~3900 rows of
  * the int8 layers or ~2600 of the bf16 ones) fails with an error and launches nothing. The call allocates nothing.
- * All calls on one GPU share its array: calls that overlap on one GPU (two streams, two threads) race. */
+ * All calls on one GPU share its array: calls that overlap on one GPU (two streams, two threads) race. The array
+ * costs 64 MiB of device memory on every GPU of a process that loads it (from the first call, when the runtime loads
+ * the code object holding it, until the process exits), whether or not the entry point is called again. */
 enum { COHERE_ENC_NOALLOC_BYTES = 64 << 20 };
 int cohere_encoder_layers_noalloc(uint16_t* x, int64_t rows, const void* const* fields, int64_t n_layers,
                                   const double* eps, const int32_t* tiles, int64_t n_tiles, const int32_t* lo,

@@ -214,11 +214,12 @@ def encode(W: dict, pieces: list[np.ndarray], threads: int = 0):
 
 
 def decode(W: dict, hidden: np.ndarray, lengths: list[int], prompt, max_new: int, forced_tokens=None,
-           threads: int = 0):
+           threads: int = 0, want_logits: bool = False):
     """Greedy decoding of every piece at once (one row per piece; rows are independent), from packed encoder output.
     forced_tokens (optional, per piece): after each step the piece's next input is this sequence's token instead of
     the checker's own pick (teacher forcing), and the checker's picks are returned beside. Returns per piece the ids
-    (prompt + generated up to and including the end token) and, with forcing, the checker's pick at every step."""
+    (prompt + generated up to and including the end token) and, with forcing, the checker's pick at every step;
+    want_logits (with forcing) adds per piece the logits row (bf16 bits) behind each of those picks."""
     D = W["decoder"]
     n, L, H = len(lengths), len(D["layers"]), D["heads"]
     mem = O.gemm_bf16(hidden, D["proj"][0], D["proj"][1], O.EPI_BIAS, threads=threads)
@@ -245,15 +246,18 @@ def decode(W: dict, hidden: np.ndarray, lengths: list[int], prompt, max_new: int
         st["tok"][s], st["plen"][s], st["limit"][s] = prompt[0], P, P - 1 + max_new
         st["cross_len"][s], st["finished"][s] = lengths[s], 0
     picks = [[] for _ in range(n)]
+    rows = [[] for _ in range(n)]
     for _ in range(P - 1 + max_new):
         running = st["finished"][:n] == 0
-        O.decoder_step(D, st, n)
+        logits = O.decoder_step(D, st, n)
         if forced_tokens is not None:
             for s in np.nonzero(running)[0]:
                 at = int(st["pos"][s])  # the position this step wrote (decoder_ops.cu:106-159)
                 if at < P:
                     continue
                 picks[s].append(int(st["tok"][s]))
+                if want_logits:
+                    rows[s].append(logits[s].copy())
                 seq_s = forced_tokens[s]
                 if at < len(seq_s):
                     t = int(seq_s[at])
@@ -268,7 +272,9 @@ def decode(W: dict, hidden: np.ndarray, lengths: list[int], prompt, max_new: int
         gen = st["out"][s, P:]
         end = np.nonzero(gen == D["eos"])[0]
         ids.append(st["out"][s, :P + (end[0] + 1 if len(end) else min(len(gen), max_new))].copy())
-    return (ids, picks) if forced_tokens is not None else ids
+    if forced_tokens is None:
+        return ids
+    return (ids, picks, [np.array(r).reshape(-1, logits.shape[1]) for r in rows]) if want_logits else (ids, picks)
 
 
 def transcribe(W: dict, pieces: list[np.ndarray], prompt, max_new: int = 448, threads: int = 0):

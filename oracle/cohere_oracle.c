@@ -50,13 +50,16 @@ static void set_threads(int nthreads) {
 }
 
 /* a1: kernels/fast_encoder.py:60-63 quantize_rows (weights, per output channel):
- * s = max(amax|w|, 1e-12) / 127; q = clamp(round_half_even(w / s), -127, 127). w holds the bf16 weights as fp32. */
+ * s = max(amax|w|, 1e-12) / 127; q = clamp(round_half_even(w / s), -127, 127). w holds the bf16 weights as fp32.
+ * The reference quantizes the weights where the model lives, on the GPU, and PyTorch's GPU division of a tensor by a
+ * Python scalar is a multiplication by the scalar's fp32 reciprocal (ATen div_true on a CPU scalar: a * (1 / b)), so
+ * the scale is max(amax, 1e-12) * fp32(1 / 127); the division w / s is tensor by tensor, a true division. */
 void orc_quantize_weight_rows(const float* w, int64_t n, int64_t k, int8_t* q, float* s) {
   for (int64_t r = 0; r < n; ++r) {
     const float* row = w + r * k;
     float mx = 0.f;
     for (int64_t c = 0; c < k; ++c) mx = fmaxf(mx, fabsf(row[c]));
-    const float sc = fmaxf(mx, 1e-12f) / 127.f;
+    const float sc = fmaxf(mx, 1e-12f) * (1.f / 127.f);
     s[r] = sc;
     for (int64_t c = 0; c < k; ++c) {
       float v = rintf(row[c] / sc);
@@ -233,7 +236,8 @@ void orc_prune_24(const float* w, int64_t n, int64_t k, float* out) {
   }
 }
 
-/* a10: kernels/stream_decoder.py:38-48 prepare_w8: per output channel s = max(amax|w|, 1e-12) / 127,
+/* a10: kernels/stream_decoder.py:38-48 prepare_w8: per output channel s = max(amax|w|, 1e-12) / 127 (on the GPU:
+ * max(amax, 1e-12) * fp32(1 / 127), as orc_quantize_weight_rows),
  * u8 = clamp(round_half_even(w / s), +-127) + 128, the bytes of every 16 along K permuted by W8_PERM (physical
  * position j holds logical k = PERM[j]). */
 static const int W8_PERM[16] = {0, 1, 8, 9, 2, 3, 10, 11, 4, 5, 12, 13, 6, 7, 14, 15};
@@ -243,7 +247,7 @@ void orc_prepare_w8(const float* w, int64_t n, int64_t k, uint8_t* q, float* s) 
     const float* row = w + r * k;
     float mx = 0.f;
     for (int64_t c = 0; c < k; ++c) mx = fmaxf(mx, fabsf(row[c]));
-    const float sc = fmaxf(mx, 1e-12f) / 127.f;
+    const float sc = fmaxf(mx, 1e-12f) * (1.f / 127.f);
     s[r] = sc;
     for (int64_t b = 0; b < k; b += 16)
       for (int j = 0; j < 16; ++j) {

@@ -12,6 +12,9 @@ advanced) are copied into the checker's, so every step is compared from identica
     percentage point, as the perturbed checker's do. With this model a perturbation of that size moves the logits
     by ~1.5 % RMS, so a few percent of the picks are near-ties (often exact bf16 ties) that either side may break;
     the measured agreement of both is printed;
+  * clear-margin rows: wherever the checker's gap between its best and second-best logit exceeds twice that step's
+    largest logit difference of the perturbed checker, the pick is not a near-tie, and the product's token must equal
+    the checker's (index-exact); the number of such rows is printed;
   * the positions advance exactly as the checker's.
 """
 
@@ -38,7 +41,10 @@ def _to_state(dec, st):
         st[b][...] = getattr(dec, a).cpu().numpy()
 
 
-def test_config3_step_tokens(gpu):
+def config3_decoder(gpu):
+    """Config 3's decoder and state on the GPU and the checker's copy: (model, dec, st, W, b). Every slot is past its
+    prompt with a self cache of U(1..448) positions of seeded int8 keys/values; the cross caches hold N(0, 1) memory's
+    keys and values (computed once on the GPU and scattered on both sides identically)."""
     from kernels.stream_decoder import StreamDecoder
 
     model = make_decoder(hidden=WIDTH, heads=HEADS, layers=LAYERS, ffn=FFN, vocab=VOCAB, seed=3, device=gpu,
@@ -79,6 +85,11 @@ def test_config3_step_tokens(gpu):
     assert b == SLOTS
     torch.cuda.synchronize()
     st["active"] = dec.active.cpu().numpy()
+    return model, dec, st, W, b
+
+
+def test_config3_step_tokens(gpu):
+    model, dec, st, W, b = config3_decoder(gpu)
     # the checker's own sensitivity: the same step from the same state with 1 % of the position-table entries moved
     # by one bf16 ulp (the size of the last-bit differences the kernels' fp32 sums make)
     W_pert = dict(W)
@@ -86,6 +97,7 @@ def test_config3_step_tokens(gpu):
     pt[np.random.default_rng(0).random(pt.shape) < 0.01] += 1
     W_pert["pos_table"] = pt
     same = same_noise = total = 0
+    clear_rows = clear_same = 0
     ratios_rms, ratios_max = [], []
     for step in range(STEPS):
         _to_state(dec, st)
@@ -102,6 +114,11 @@ def test_config3_step_tokens(gpu):
         got_tok, want_tok = dec.tok[:SLOTS].cpu().numpy(), st["tok"][:SLOTS]
         step_same, step_noise = int((got_tok == want_tok).sum()), int((st_p["tok"][:SLOTS] == want_tok).sum())
         same, same_noise, total = same + step_same, same_noise + step_noise, total + SLOTS
+        top2 = np.sort(want, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2.0 * dn.max()
+        clear_rows += int(clear.sum())
+        clear_same += int((got_tok == want_tok)[clear].sum())
+        assert np.array_equal(got_tok[clear], want_tok[clear]), (step, np.nonzero(clear & (got_tok != want_tok))[0])
         print(f"step {step}: logits rms diff {np.sqrt(np.mean(d ** 2)) / rms:.2e} max {d.max() / rms:.2e} x RMS "
               f"(perturbed checker {np.sqrt(np.mean(dn ** 2)) / rms:.2e} / {dn.max() / rms:.2e}); tokens equal: "
               f"kernels {step_same}/{SLOTS}, perturbed checker {step_noise}/{SLOTS}", flush=True)
@@ -112,6 +129,6 @@ def test_config3_step_tokens(gpu):
         assert np.array_equal(dec.pos[:SLOTS].cpu().numpy(), st["pos"][:SLOTS]), step
     print(f"tokens: kernels {same} / {total} index-exact with the checker, perturbed checker {same_noise} / {total}; "
           f"logit difference vs the perturbed checker's: rms x{max(ratios_rms):.2f}, max x{max(ratios_max):.2f} "
-          f"(worst step)", flush=True)
+          f"(worst step); clear-margin rows {clear_same} / {clear_rows} index-exact", flush=True)
     assert max(ratios_rms) <= 1.5 and max(ratios_max) <= 2.0
     assert same >= same_noise - 0.01 * total

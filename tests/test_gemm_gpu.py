@@ -276,6 +276,53 @@ def test_sparse_silu_q8_equals_dense(ext):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("M,N,K,group", [(3000, 5120, 1280, 1280), (3000, 1280, 5120, 5120), (3000, 1280, 5120, 256),
+                                         (37, 512, 384, 128)])
+def test_sparse_tiled_layout_same_bits(ext, M, N, K, group):
+    """gemm_sp_tiled on pack_24_tiled's layout gives the bits of gemm_sp_epi on compress_24's, for every epilogue
+    (int32 sums, BIAS, RESID in place, GLU, SILU_Q8) and, on the small shape, for every gfx950 tile."""
+    from kernels.cuda_ext import EPI_BIAS, EPI_GLU, EPI_I32, EPI_RESID, EPI_SILU_Q8
+    from kernels.sparse import pack_24_tiled
+
+    print(f"gemm_sp_tiled M={M} N={N} K={K} group={group}", flush=True)
+    _, xq, _, _, _, _ = _prep(M, 64, K, seed=31)
+    xs = (torch.rand(M, K // group, generator=torch.Generator().manual_seed(32)) * 0.02 + 0.001).cuda()
+    wq, ws, wc, e, b = _sparse_weights(N, K, seed=33)
+    wt = pack_24_tiled(wc, e)
+    r = torch.randn(M, N, generator=torch.Generator().manual_seed(34)).to(torch.bfloat16).cuda()
+
+    def both(epi, dtype, width, qs_cols=0):
+        outs = []
+        for tiled in (False, True):
+            out = (r[:, :width].clone() if epi == EPI_RESID else torch.empty(M, width, dtype=dtype, device="cuda"))
+            qs = torch.empty(M, qs_cols, dtype=torch.float32, device="cuda") if qs_cols else None
+            resid = out if epi == EPI_RESID else None
+            if tiled:
+                ext.gemm_sp_tiled(xq, xs, group, wt, ws, b, out, epi, resid, 0.5, qs, -1)
+            else:
+                ext.gemm_sp_epi(xq, xs, group, wc, e, ws, b, out, epi, resid, 0.5, qs, -1)
+            outs.append((out, qs))
+        torch.cuda.synchronize()
+        raw = lambda t: t.view(torch.int16) if t.dtype == torch.bfloat16 else t  # noqa: E731
+        assert torch.equal(raw(outs[0][0]), raw(outs[1][0])), epi
+        if qs_cols:
+            assert torch.equal(outs[0][1], outs[1][1]), epi
+
+    tiles = range(ext.set_gemm_tile(-1)) if M < 100 else [-1]
+    try:
+        for tile in tiles:
+            ext.set_gemm_tile(tile)
+            if group == K:
+                both(EPI_I32, torch.int32, N)
+            both(EPI_BIAS, torch.bfloat16, N)
+            both(EPI_RESID, torch.bfloat16, N)
+            both(EPI_GLU, torch.bfloat16, N // 2)
+            if N % 256 == 0:
+                both(EPI_SILU_Q8, torch.int8, N, N // 256)
+    finally:
+        ext.set_gemm_tile(-1)
+
+
 def test_empty_rows_noop(ext):
     from kernels.cuda_ext import EPI_BIAS
 

@@ -143,3 +143,34 @@ def test_weight_quantizers_match_oracle():
     uo, s8o = O.prepare_w8(bf16_bits(w))
     assert np.array_equal(u.numpy(), uo) and np.array_equal(s8.numpy(), s8o)
     assert np.array_equal(unprepare_w8(u).numpy(), qo)
+
+
+def test_pack_24_tiled_matches_c_abi_and_round_trips():
+    """The stage-tiled 2:4 layout: kernels.sparse.pack_24_tiled (torch) and the library's cohere_pack_24_tiled (host
+    loops) give the same bytes, and every record decodes back to compress_24's kept values and selectors through the
+    layout's own definition (chunk i = row i // 4, logical chunk (i % 4) ^ ((i // 8) % 4); selectors at 1024 + 16 r)."""
+    from kernels.cuda_ext import _lib as lib
+    from kernels.sparse import TILED_REC, compress_24, pack_24_tiled, prune_24_magnitude
+
+    g = torch.Generator().manual_seed(5)
+    N, K = 48, 384
+    w = prune_24_magnitude(torch.randn(N, K, generator=g))
+    q = (torch.randint(-127, 128, (N, K), generator=g) * (w != 0)).to(torch.int8)
+    kept, words = compress_24(q)
+    t = pack_24_tiled(kept, words)
+    assert tuple(t.shape) == (N // 16, K // 128, TILED_REC)
+    assert lib.cohere_pack_24_tiled_bytes(N, K) == t.numel() and lib.cohere_pack_24_tiled_bytes(40, K) == -1
+    out = np.zeros(t.numel(), np.uint8)
+    assert lib.cohere_pack_24_tiled(kept.numpy().ctypes.data, words.numpy().ctypes.data, N, K, out.ctypes.data) == 0
+    assert np.array_equal(out, t.numpy().reshape(-1))
+    tn = t.numpy()
+    back_k, back_e = np.zeros_like(kept.numpy()), np.zeros_like(words.numpy())
+    for rb in range(N // 16):
+        for kt in range(K // 128):
+            rec = tn[rb, kt]
+            for i in range(64):
+                r, c = rb * 16 + i // 4, (i % 4) ^ ((i // 8) % 4)
+                back_k[r, kt * 64 + c * 16:kt * 64 + c * 16 + 16] = rec[16 * i:16 * i + 16].view(np.int8)
+            for r in range(16):
+                back_e[rb * 16 + r, kt * 4:kt * 4 + 4] = rec[1024 + 16 * r:1040 + 16 * r].view(np.int32)
+    assert np.array_equal(back_k, kept.numpy()) and np.array_equal(back_e, words.numpy())

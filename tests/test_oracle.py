@@ -91,9 +91,14 @@ def test_quantize_weight_rows_matches_torch_and_bounds():
     w[5] = 0  # zero row: scale 1e-12 / 127, q = 0
     q, s = O.quantize_weight_rows(bf16_bits(w))
     wf = w.float()
-    st = wf.abs().amax(-1).clamp_min(1e-12) / 127
+    # the scale as the reference's GPU computes `amax / 127`: times fp32(1 / 127) (pinned against PyTorch's own GPU
+    # division in tests/test_quant_gpu.py); CPU PyTorch divides exactly, which differs on some rows
+    rcp = float(np.float32(1.0) / np.float32(127.0))
+    st = wf.abs().amax(-1).clamp_min(1e-12) * rcp
     qt = torch.round(wf / st[:, None]).clamp(-127, 127).to(torch.int8)
     assert np.array_equal(s, st.numpy()) and np.array_equal(q, qt.numpy())
+    exact = wf.abs().amax(-1).clamp_min(1e-12) / 127
+    assert (exact != st).any()  # the two forms are told apart by this input
     assert (np.abs(q).max(1)[np.arange(96) != 5] == 127).all() and not q[5].any()
     err = np.abs(q.astype(np.float64) * s[:, None] - bf16_float(bf16_bits(w)))
     assert (err <= s[:, None].astype(np.float64) * (0.5 + 1e-5)).all()

@@ -9,7 +9,12 @@ sensitivity, measured on the same input: the checker run again with 1 % of its l
     checker's;
   * tokens: decoding with the GPU's tokens as history (teacher forcing), the checker picks the GPU's next token at
     least as often, less two points, as it picks its own next token when decoding from the perturbed checker's
-    encoder output with its own tokens as history. Both agreements are printed.
+    encoder output with its own tokens as history. Both agreements are printed;
+  * clear-margin picks: the checker also decodes from the perturbed encoder output with the GPU's tokens as history,
+    so that both of its runs see the same history and their logits can be compared step by step. Wherever the
+    checker's gap between its best and second-best logit exceeds twice that step's largest logit difference between
+    its two runs, the pick is not a near-tie and the kernels' token must equal the checker's. The number of such picks
+    is printed.
 """
 
 from __future__ import annotations
@@ -67,7 +72,8 @@ def test_config4_pipeline_against_checker_chain(gpu):
     assert d_gpu <= 1.5 * d_noise
 
     own = chain.decode(W, hidden, lengths, prompt, MAX_NEW)
-    _, picks_gpu = chain.decode(W, hidden, lengths, prompt, MAX_NEW, forced_tokens=got)
+    _, picks_gpu, rows_gpu = chain.decode(W, hidden, lengths, prompt, MAX_NEW, forced_tokens=got, want_logits=True)
+    _, _, rows_pert = chain.decode(W, hidden_p, lengths, prompt, MAX_NEW, forced_tokens=got, want_logits=True)
     _, picks_noise = chain.decode(W, hidden_p, lengths, prompt, MAX_NEW, forced_tokens=own)
     a_gpu, n_gpu = _agreement(picks_gpu, got, len(prompt))
     a_noise, n_noise = _agreement(picks_noise, own, len(prompt))
@@ -76,3 +82,14 @@ def test_config4_pipeline_against_checker_chain(gpu):
     print(f"tokens (teacher-forced): checker agrees with the kernels on {a_gpu:.4f} of {n_gpu}, with itself from the "
           f"perturbed encoder output on {a_noise:.4f} of {n_noise}; free-running common prefixes {free}", flush=True)
     assert a_gpu >= a_noise - 0.02
+    clear_n = clear_same = 0
+    for s, (pk, toks, rg, rp) in enumerate(zip(picks_gpu, got, rows_gpu, rows_pert)):
+        n = min(len(pk), len(toks) - len(prompt), len(rg), len(rp))
+        lg, lp = bf16_float(rg[:n]).astype(np.float64), bf16_float(rp[:n]).astype(np.float64)
+        top2 = np.sort(lg, axis=1)[:, -2:]
+        clear = (top2[:, 1] - top2[:, 0]) > 2.0 * np.abs(lp - lg).max(axis=1)
+        gen = np.asarray(toks[len(prompt):len(prompt) + n])
+        ok = np.asarray(pk[:n]) == gen
+        clear_n, clear_same = clear_n + int(clear.sum()), clear_same + int(ok[clear].sum())
+        assert ok[clear].all(), (s, np.nonzero(clear & ~ok)[0])
+    print(f"clear-margin picks: {clear_same} / {clear_n} index-exact", flush=True)
