@@ -762,7 +762,9 @@ void launch_tile(const GemmArgs& args, hipStream_t s) {
   // the feed-forward W2's grouping (256 K per scale) runs the static-group loop (tiles of one wave per SIMD: with
   // two, its unrolled groups do not fit the registers)
   constexpr int GS = 256 / Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::KSTEP;
-  if constexpr (GROUPED && EPI == EPI_RESID && WM * WN <= 4) {
+  if constexpr (GROUPED && EPI == EPI_RESID &&
+                (WM * WN <= 4 || Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::MI * Tile<BM, BN, WM, WN, ST, MS,
+                                                                                       GROUPED, SPARSE>::NI <= 8)) {
     if (p.group == 256 && p.K / 256 <= Tile<BM, BN, WM, WN, ST, MS, GROUPED, SPARSE>::GMAX) {  // scales all in LDS
       gemm_q8_kernel<BM, BN, WM, WN, ST, MS, EPI, GROUPED, SPARSE, GS><<<grid, WM * WN * 64, 0, s>>>(p);
       return;
@@ -775,7 +777,8 @@ void launch_tile(const GemmArgs& args, hipStream_t s) {
 //   0 128x128 (2x2, 4)   1 128x256 (2x2, 3)   2 256x128 (2x2, 3)   3 64x128 (2x2, 4)   4 64x256 (1x4, 3)
 //   5 32x128 (1x4, 4)    6 256x256 (2x4, 2 dense / 3 sparse)        7 64x64 (2x2, 4)    8 256x128 (4x2, 3)
 //   9 128x256 (2x4, 3)   10 256x256 (4x2, 2 dense / 3 sparse)   11 256x128 (2x2, 3)   12 128x128 (2x2, 4)
-//   13 128x256 (2x2, 3)   14 256x256 (2x2, 2 dense / 3 sparse)   15 256x256 (4x4: 16 waves, 2 dense / 3 sparse);
+//   13 128x256 (2x2, 3)   14 256x256 (2x2, 2 dense / 3 sparse)   15 256x256 (4x4: 16 waves, 2 dense / 3 sparse)
+//   16 128x128 (4x2: 8 waves of 32 tokens x 64 channels, 4)   17 128x128 (2x4: 8 waves of 64 tokens x 32 channels, 4);
 //   tiles 11-13 use the 32x32 matrix instructions, the others 16x16
 struct TileInfo {
   int bm, bn;
@@ -784,7 +787,8 @@ struct TileInfo {
 constexpr TileInfo TILES[] = {{128, 128, true}, {128, 256, false}, {256, 128, false}, {64, 128, true},
                               {64, 256, true},  {32, 128, true},   {256, 256, false}, {64, 64, true},
                               {256, 128, true}, {128, 256, true},  {256, 256, false}, {256, 128, false},
-                              {128, 128, true}, {128, 256, false}, {256, 256, false}, {256, 256, false}};
+                              {128, 128, true}, {128, 256, false}, {256, 256, false}, {256, 256, false},
+                              {128, 128, true}, {128, 128, true}};
 constexpr int N_TILES = sizeof(TILES) / sizeof(TILES[0]);
 
 // launches tile `tile` for one (SPARSE, EPI, GROUPED); false when the tile has no such instantiation
@@ -799,6 +803,8 @@ bool launch_tiles(int tile, const GemmArgs& p, hipStream_t s) {
     case 8: launch_tile<256, 128, 4, 2, 3, 16, EPI, GROUPED, SPARSE>(p, s); return true;
     case 9: launch_tile<128, 256, 2, 4, 3, 16, EPI, GROUPED, SPARSE>(p, s); return true;
     case 12: launch_tile<128, 128, 2, 2, 4, 32, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 16: launch_tile<128, 128, 4, 2, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
+    case 17: launch_tile<128, 128, 2, 4, 4, 16, EPI, GROUPED, SPARSE>(p, s); return true;
     default: break;
   }
   if constexpr (!GROUPED) {

@@ -44,12 +44,18 @@ int choose_tile(const GemmArgs& p, bool grouped, bool bf = false) {
   // The int8 256x256 tile runs 16 waves (15) in place of 8 (6), four per SIMD hiding more latency: SILU_Q8's
   // VALU-heavy epilogue 31.7 -> 30.3 us at config 1; with the grid split into one part per XCD, the bias epilogue too
   // (config 1 up 22.8 -> 21.9 us, config 0 dense 24.5 -> 24.1 us)
+  // The stage-tiled 2:4 weights (contiguous kilobyte loads) move the balance: there the 8-wave 256x256 tile (10)
+  // beats the 16-wave one (config 1 up 23.9 -> 22.0 us, SILU_Q8 31.4 -> 30.7) and the 16x16 128x128 tile (0) its
+  // 32x32 twin (config 1 down 22.8 -> 22.4 us), alternating runs.
   static const int order[] = {6, 9, 1, 8, 2, 12, 0, 4, 3, 5, 7};
   const int64_t want = (int64_t)num_cus() * 64 / 100;
   int best = -1;
   for (int id0 : order) {
-    const int id = id0 == 6 && !bf ? 15 : id0;
-    if (!fits(id) || (grouped && (id == 12 || id == 8 || id == 9))) continue;
+    // grouped scales take the 8-wave 128x128 tile (17: 64 tokens x 32 channels a wave, two waves per SIMD) in place
+    // of the 4-wave one: the per-group fold's VALU work of one wave then overlaps the other's matrix instructions
+    // (config-2 feed-forward W2, 3000 x 1280 x 5120 in groups of 256, 2:4: 33.4 -> 29.3 us)
+    const int id = id0 == 6 && !bf ? (p.tiled ? 10 : 15) : (id0 == 0 && grouped ? 17 : id0);
+    if (!fits(id) || (grouped && (id == 12 || id == 8 || id == 9)) || (p.tiled && id == 12)) continue;
     if (tiles_of(id) >= want) return id;
     if (best < 0 || tiles_of(id) > tiles_of(best)) best = id;
   }
