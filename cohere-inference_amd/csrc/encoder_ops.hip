@@ -11,6 +11,7 @@
 #include "common.h"
 
 #include <string>
+#include <type_traits>
 
 namespace {
 
@@ -140,7 +141,8 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
 //                   own 8 probabilities: the 32 keys are ordered so that k slot b of lane group g is key 4g + b for
 //                   b < 4 and 16 + 4g + b - 4 after -- the same key order on both operands)
 // with v_mfma_f32_16x16x32_bf16 (lane l: row/col l % 16, k = 8 (l / 16) + b; result element e of lane l: row
-// 4 (l / 16) + e, col l % 16). Keys stream in tiles of 32 with an online softmax in fp32. The position term a key tile
+// 4 (l / 16) + e, col l % 16); a head size that is an odd multiple of 16 ends with one v_mfma_f32_16x16x16_bf16 step
+// (k = 4 (l / 16) + b). Keys stream in tiles of 32 with an online softmax in fp32. The position term a key tile
 // needs spans 95 distances; each wave computes its own 48 (3 blocks of 16) from a ring of 128 table rows in LDS, of
 // which each key tile adds 32, rounds them as the module does and gathers its scores from them through a small
 // per-wave LDS buffer.
@@ -148,13 +150,15 @@ constexpr int AT_Q = 64, AT_KEYS = 32, AT_RING = 128, AT_PW = 52;  // per-wave p
 
 template <int D>
 struct AttnShape {
-  static constexpr int KS = (D + 31) / 32;    // k steps of 32 over the head size (the last one zero-padded)
-  static constexpr int DK = KS * 32;          // the head size padded to whole k steps; columns D .. DK stay zero
-  static constexpr int DP = DK + 8;           // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
+  static constexpr bool TAIL = D % 32 != 0;   // one last k step of 16
+  static constexpr int KS = D / 32;           // k steps of 32
+  static constexpr int DP = D + 8;            // LDS row of K / R tiles (elements; 16-byte aligned, off bank stride)
   static constexpr int OB = D / 16;           // 16-dim blocks of the output
   static constexpr int VT = AT_KEYS + 4;      // LDS row of the transposed value tile
+  // key and value tiles double-buffered where three workgroups still fit a CU's 160 KB (one barrier per key tile)
+  static constexpr int NBUF = D <= 96 ? 2 : 1;
   static constexpr int K_ELEMS = AT_KEYS * DP, V_ELEMS = D * VT, R_ELEMS = AT_RING * DP, P_ELEMS = 4 * 16 * AT_PW;
-  static constexpr int LDS_BYTES = 2 * (K_ELEMS + V_ELEMS + R_ELEMS + P_ELEMS);
+  static constexpr int LDS_BYTES = 2 * (NBUF * (K_ELEMS + V_ELEMS) + R_ELEMS + P_ELEMS);
   static_assert(D % 16 == 0, "head size");
 };
 
@@ -169,36 +173,71 @@ struct AttnArgs {
   float scale;
 };
 
-// 8 bf16 of an LDS row as an MFMA operand (past the head size the row's padding columns, kept zero)
-template <int D>
-DEVI v8bf lds_op(const uint16_t* row, int col) {
-  return *reinterpret_cast<const v8bf*>(row + col);
+typedef short v4s __attribute__((ext_vector_type(4)));
+
+// 16 bytes at element offset off of a uniform base: a 32-bit byte offset from the base in scalar registers
+DEVI uint4 ld16(const uint16_t* base, uint32_t off) {
+  return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + (off << 1));
 }
 
-// bf16(q + bias) for dims col .. col + 7 of one query row (zero past the head size or for rows past the sequence)
-template <int D>
-DEVI v8bf q_plus(const uint16_t* qrow, const uint16_t* bias, int col, bool valid) {
-  if (!valid || (D % 32 != 0 && col >= D)) return v8bf{};
-  const uint4 qv = *reinterpret_cast<const uint4*>(qrow + col), bv = *reinterpret_cast<const uint4*>(bias + col);
-  const uint32_t qa[4] = {qv.x, qv.y, qv.z, qv.w}, ba[4] = {bv.x, bv.y, bv.z, bv.w};
-  v8bf r;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    r[2 * k] = (__bf16)(bf_lo(qa[k]) + bf_lo(ba[k]));
-    r[2 * k + 1] = (__bf16)(bf_hi(qa[k]) + bf_hi(ba[k]));
+// bf16(q + bias) for dims col .. col + N - 1 of one query row (zero for rows past the sequence), N = 8 or 4
+template <int N>
+DEVI void q_plus(const uint16_t* qrow, const uint16_t* bias, int col, bool valid, uint16_t* __restrict__ r) {
+  uint32_t qa[N / 2], ba[N / 2];
+  if constexpr (N == 8) {
+    const uint4 qv = *reinterpret_cast<const uint4*>(qrow + col), bv = *reinterpret_cast<const uint4*>(bias + col);
+    qa[0] = qv.x, qa[1] = qv.y, qa[2] = qv.z, qa[3] = qv.w, ba[0] = bv.x, ba[1] = bv.y, ba[2] = bv.z, ba[3] = bv.w;
+  } else {
+    const uint2 qv = *reinterpret_cast<const uint2*>(qrow + col), bv = *reinterpret_cast<const uint2*>(bias + col);
+    qa[0] = qv.x, qa[1] = qv.y, ba[0] = bv.x, ba[1] = bv.y;
   }
-  return r;
+#pragma unroll
+  for (int k = 0; k < N / 2; ++k) {
+    const uint32_t v = pack_bf2(bf_lo(qa[k]) + bf_lo(ba[k]), bf_hi(qa[k]) + bf_hi(ba[k]));
+    reinterpret_cast<uint32_t*>(r)[k] = valid ? v : 0u;
+  }
 }
 
+// one 16-row block of a product over the head size: acc += A rows (LDS, row pointer per lane) . B (registers)
 template <int D>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 80 ? 4 : 1, D == 80 ? 4 : 8)))
+struct HeadDot {
+  using S = AttnShape<D>;
+  v8bf b[S::KS];
+  v4s bt;  // the last 16 dims when the head size is an odd multiple of 16
+  DEVI void load(const uint16_t* qrow, const uint16_t* bias, int g, bool valid) {
+#pragma unroll
+    for (int ks = 0; ks < S::KS; ++ks) {
+      uint16_t r[8];
+      q_plus<8>(qrow, bias, ks * 32 + g * 8, valid, r);
+      b[ks] = __builtin_bit_cast(v8bf, *reinterpret_cast<const uint4*>(r));
+    }
+    if constexpr (S::TAIL) {
+      uint16_t r[4];
+      q_plus<4>(qrow, bias, S::KS * 32 + g * 4, valid, r);
+      bt = __builtin_bit_cast(v4s, *reinterpret_cast<const uint2*>(r));
+    }
+  }
+  DEVI v4f step(const uint16_t* row, int g, int ks, v4f acc) const {
+    if (ks < S::KS)
+      return __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const v8bf*>(row + ks * 32 + g * 8), b[ks], acc,
+                                                     0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(*reinterpret_cast<const v4s*>(row + S::KS * 32 + g * 4), bt, acc,
+                                                      0, 0, 0);
+  }
+  static constexpr int steps = S::KS + (S::TAIL ? 1 : 0);
+};
+
+// Head size 80 keeps the register budget of four waves per SIMD (128 VGPRs) although its LDS admits three
+// workgroups per CU: the compiler's schedule within 168 registers ran slower.
+template <int D>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 96 ? 4 : 1, D <= 96 ? 4 : 8)))
 relpos_attention_kernel(const AttnArgs p) {
   using S = AttnShape<D>;
   __shared__ __attribute__((aligned(16))) uint16_t lds[S::LDS_BYTES / 2];
-  uint16_t* sK = lds;                      // [32 keys][DP]
-  uint16_t* sVt = sK + S::K_ELEMS;         // [D dims][VT]
-  uint16_t* sR = sVt + S::V_ELEMS;         // [128 ring slots][DP], slot = table row & 127
-  uint16_t* sP = sR + S::R_ELEMS;          // [4 waves][16 queries][AT_PW]
+  uint16_t* sK0 = lds;                             // [NBUF][32 keys][DP]
+  uint16_t* sV0 = sK0 + S::NBUF * S::K_ELEMS;      // [NBUF][D dims][VT]
+  uint16_t* sR = sV0 + S::NBUF * S::V_ELEMS;       // [128 ring slots][DP], slot = table row & 127
+  uint16_t* sP = sR + S::R_ELEMS;                  // [4 waves][16 queries][AT_PW]
 
   // XCD-aware order: workgroup b runs on XCD b % 8, so each XCD takes a contiguous run of (head, tile) items, tiles
   // innermost: the query tiles of one sequence and head share their keys, values and table rows in that XCD's L2
@@ -210,76 +249,86 @@ relpos_attention_kernel(const AttnArgs p) {
   const int HD = p.H * D, ld = 3 * HD;
   uint16_t* sPw = sP + w * 16 * AT_PW;
 
-  // this lane's query, as the B operand of both products
+  // this lane's query plus either bias, as the B operand of both products
   const int qrow = q0 + 16 * w + iq;
   const bool qvalid = qrow < len;
   const uint16_t* qptr = p.qkv + (int64_t)(start + (qvalid ? qrow : 0)) * ld + h * D;
-  v8bf qu[S::KS], qvb[S::KS];
-#pragma unroll
-  for (int ks = 0; ks < S::KS; ++ks) {
-    qu[ks] = q_plus<D>(qptr, p.bu + h * D, ks * 32 + g * 8, qvalid);
-    qvb[ks] = q_plus<D>(qptr, p.bv + h * D, ks * 32 + g * 8, qvalid);
-  }
-
-  // the K and table rows' columns D .. DK: zero for good (the tiles write columns below D only); published by the
-  // first tile's barrier
-  if constexpr (S::DK > D) {
-    constexpr int PADC = (S::DK - D) / 8;  // 16-byte chunks of padding per row
-    for (int id = tid; id < (AT_KEYS + AT_RING) * PADC; id += 256) {
-      const int row = id / PADC, c = D + (id % PADC) * 8;
-      uint16_t* dst = row < AT_KEYS ? sK + row * S::DP + c : sR + (row - AT_KEYS) * S::DP + c;
-      *reinterpret_cast<uint4*>(dst) = make_uint4(0, 0, 0, 0);
-    }
-  }
+  HeadDot<D> qu, qv;
+  qu.load(qptr, p.bu + h * D, g, qvalid);
+  qv.load(qptr, p.bv + h * D, g, qvalid);
 
   v4f o[S::OB];
 #pragma unroll
   for (int i = 0; i < S::OB; ++i) o[i] = v4f{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
+  float m = -INFINITY, l = 0.f;  // running maximum (natural units) and sum of this lane's query
 
   const uint16_t* kbase = p.qkv + (int64_t)start * ld + HD + h * D;
   const uint16_t* vbase = kbase + HD;
   const uint16_t* rbase = p.rk + h * D;
   constexpr int CH = D / 8;  // 16-byte chunks per row
-  // a key tile's global data: keys j0 .. j0 + 31 (clamped to the sequence), their values, and the 32 table rows of
-  // distances q0 - j0 - 31 .. q0 - j0 (the tile reads distances up to q0 - j0 + 63; the previous tiles brought
-  // those). Loaded into registers one tile ahead, so the loads of tile j0 + 32 fly while tile j0 computes.
-  constexpr int NC = (AT_KEYS * CH + 255) / 256;  // 16-byte chunks per thread and array
-  uint4 pk[NC], pv[NC], pr[NC];
+  // a key tile's global data: keys j0 .. j0 + 31, their values, and the 32 table rows of distances
+  // q0 - j0 - 31 .. q0 - j0 (the tile reads distances up to q0 - j0 + 63; the previous tiles brought those). Loaded
+  // into registers one tile ahead, so the loads of tile j0 + 32 fly while tile j0 computes. Chunk item x of a thread
+  // is (row id / CH, chunk id % CH) for keys and table rows; for values it is (key pair item % 16, chunk item / 16),
+  // so that the pair's 8 dims go to LDS as 8 dwords of the transposed tile with the lanes of a wave on distinct
+  // banks. 32-bit element offsets from uniform bases (a layer's qkv and table stay below 2^31 elements); keys past
+  // the sequence load its last key (their scores are masked and their probabilities exactly 0, the values finite, so
+  // no register is zeroed) and table rows are clamped to the table.
+  constexpr int NC = (AT_KEYS * CH + 255) / 256;      // key / table chunks per thread
+  constexpr int NV = (AT_KEYS / 2 * CH + 255) / 256;  // value chunk pairs per thread
+  uint4 pk[NC], pr[NC], pw[NV][2];
 #pragma unroll
-  for (int x = 0; x < NC; ++x) pk[x] = pv[x] = pr[x] = make_uint4(0, 0, 0, 0);  // once: the chunks past 32 rows
+  for (int x = 0; x < NC; ++x) pk[x] = pr[x] = make_uint4(0, 0, 0, 0);  // once: the chunks past 32 rows
+#pragma unroll
+  for (int x = 0; x < NV; ++x) pw[x][0] = pw[x][1] = make_uint4(0, 0, 0, 0);
   auto fetch = [&](int j0) {
+    const int d0 = q0 - j0 - (AT_KEYS - 1) + p.rel_off;  // table row of the tile's first new distance
 #pragma unroll
     for (int x = 0; x < NC; ++x) {
       const int id = tid + x * 256;
       if (id < AT_KEYS * CH) {
-        // 32-bit element offsets from uniform bases (a layer's qkv and table stay below 2^31 elements). Keys past
-        // the sequence load its last key: their scores are masked and their probabilities exactly 0 (the values
-        // finite), so no register is zeroed
         const int r = id / CH, c = (id % CH) * 8, key = min(j0 + r, len - 1);
-        const uint32_t off = (uint32_t)key * (uint32_t)ld + (uint32_t)c;
-        pk[x] = *reinterpret_cast<const uint4*>(kbase + off);
-        pv[x] = *reinterpret_cast<const uint4*>(vbase + off);
-        const int d = q0 - j0 - (AT_KEYS - 1) + r, trow = min(max(d + p.rel_off, 0), p.rel_rows - 1);
-        pr[x] = *reinterpret_cast<const uint4*>(rbase + ((uint32_t)trow * (uint32_t)HD + (uint32_t)c));
+        pk[x] = ld16(kbase, (uint32_t)key * (uint32_t)ld + (uint32_t)c);
+        const int trow = min(max(d0 + r, 0), p.rel_rows - 1);
+        pr[x] = ld16(rbase, (uint32_t)trow * (uint32_t)HD + (uint32_t)c);
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < NV; ++x) {
+      const int item = tid + x * 256;
+      if (item < AT_KEYS / 2 * CH) {
+        const int rp = item % 16, c = (item / 16) * 8;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int key = min(j0 + 2 * rp + k, len - 1);
+          pw[x][k] = ld16(vbase, (uint32_t)key * (uint32_t)ld + (uint32_t)c);
+        }
       }
     }
   };
-  auto stash = [&](int j0) {
+  auto stash = [&](int j0, uint16_t* sK, uint16_t* sVt) {
 #pragma unroll
     for (int x = 0; x < NC; ++x) {
       const int id = tid + x * 256;
       if (id < AT_KEYS * CH) {
         const int r = id / CH, c = (id % CH) * 8;
         *reinterpret_cast<uint4*>(sK + r * S::DP + c) = pk[x];
-        const uint32_t va[4] = {pv[x].x, pv[x].y, pv[x].z, pv[x].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          sVt[(c + 2 * k) * S::VT + r] = (uint16_t)(va[k] & 0xffff);
-          sVt[(c + 2 * k + 1) * S::VT + r] = (uint16_t)(va[k] >> 16);
-        }
         const int d = q0 - j0 - (AT_KEYS - 1) + r;
         *reinterpret_cast<uint4*>(sR + ((d + p.rel_off) & (AT_RING - 1)) * S::DP + c) = pr[x];
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < NV; ++x) {
+      const int item = tid + x * 256;
+      if (item < AT_KEYS / 2 * CH) {
+        const int rp = item % 16, c = (item / 16) * 8;
+        const uint32_t a[4] = {pw[x][0].x, pw[x][0].y, pw[x][0].z, pw[x][0].w};
+        const uint32_t b[4] = {pw[x][1].x, pw[x][1].y, pw[x][1].z, pw[x][1].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          *reinterpret_cast<uint32_t*>(sVt + (c + 2 * k) * S::VT + 2 * rp) = (a[k] & 0xffffu) | (b[k] << 16);
+          *reinterpret_cast<uint32_t*>(sVt + (c + 2 * k + 1) * S::VT + 2 * rp) = (a[k] >> 16) | (b[k] & 0xffff0000u);
+        }
       }
     }
   };
@@ -290,58 +339,67 @@ relpos_attention_kernel(const AttnArgs p) {
     *reinterpret_cast<uint4*>(sR + ((d + p.rel_off) & (AT_RING - 1)) * S::DP + c) =
         *reinterpret_cast<const uint4*>(p.rk + (int64_t)trow * HD + h * D + c);
   }
-  fetch(0);
-  for (int j0 = 0; j0 < len; j0 += AT_KEYS) {
-    stash(j0);
-    __syncthreads();
-    if (j0 + AT_KEYS < len) fetch(j0 + AT_KEYS);
 
-    // content scores of keys kb * 16 + 4 g + e for this lane's query
-    v4f s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = v4f{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* krow = sK + (kb * 16 + iq) * S::DP;
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks)
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_op<D>(krow, ks * 32 + g * 8), qu[ks], s[kb], 0, 0, 0);
-    }
-    // position term of this wave's queries: distances dw0 + db, db < 48, rounded as the module rounds it
+  // one key tile from the given key and value buffers: scores, the online softmax and the value product
+  constexpr float L2E = 1.4426950408889634f;
+  auto key_tile = [&](int j0, const uint16_t* sK, const uint16_t* sVt) {
+    // position term of this wave's queries: distances dw0 + db, db < 48 (3 blocks of 16), its three products
+    // interleaved per k step; then the content scores of keys kb * 16 + 4 g + e while those finish
     const int dw0 = q0 + 16 * w - j0 - (AT_KEYS - 1);
+    const uint16_t* rrow[3];
+#pragma unroll
+    for (int pb = 0; pb < 3; ++pb) rrow[pb] = sR + ((dw0 + pb * 16 + iq + p.rel_off) & (AT_RING - 1)) * S::DP;
+    v4f acc[3], s[2];
+#pragma unroll
+    for (int pb = 0; pb < 3; ++pb) acc[pb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < HeadDot<D>::steps; ++ks)
+#pragma unroll
+      for (int pb = 0; pb < 3; ++pb) acc[pb] = qv.step(rrow[pb], g, ks, acc[pb]);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s[kb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < HeadDot<D>::steps; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) s[kb] = qu.step(sK + (kb * 16 + iq) * S::DP, g, ks, s[kb]);
+    // the position scores rounded as the module rounds them, to the wave's buffer
 #pragma unroll
     for (int pb = 0; pb < 3; ++pb) {
-      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
-      const uint16_t* rrow = sR + ((dw0 + pb * 16 + iq + p.rel_off) & (AT_RING - 1)) * S::DP;
-#pragma unroll
-      for (int ks = 0; ks < S::KS; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lds_op<D>(rrow, ks * 32 + g * 8), qvb[ks], acc, 0, 0, 0);
       uint2 u;
-      u.x = pack_bf2(round_bf(acc[0]) * p.scale, round_bf(acc[1]) * p.scale);
-      u.y = pack_bf2(round_bf(acc[2]) * p.scale, round_bf(acc[3]) * p.scale);
+      u.x = pack_bf2(round_bf(acc[pb][0]) * p.scale, round_bf(acc[pb][1]) * p.scale);
+      u.y = pack_bf2(round_bf(acc[pb][2]) * p.scale, round_bf(acc[pb][3]) * p.scale);
       *reinterpret_cast<uint2*>(sPw + iq * AT_PW + pb * 16 + g * 4) = u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's position rows, written by other lanes
+    // the 8 position scores of this lane, read together (the addresses lie inside the wave's buffer for every key;
+    // the empty asm keeps the compiler from moving each read under the key mask, one after another)
+    float pos[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) pos[k] = bf2f(sPw[iq * AT_PW + iq - ((k >> 2) * 16 + g * 4 + (k & 3)) + AT_KEYS - 1]);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(pos[k]));
 
-    // scores, masked past the sequence; online softmax per query (the 4 lane groups hold its 32 keys)
+    // scores (masked past the sequence in the last tile); online softmax per query (the 4 lane groups hold its
+    // 32 keys). exp(v - mx) is taken as exp2(v log2 e - mx log2 e).
     float sv[8], mx = m;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int jk = kb * 16 + g * 4 + e;
-        float v = -INFINITY;
-        if (j0 + jk < len) v = __builtin_fmaf(s[kb][e], p.scale, bf2f(sPw[iq * AT_PW + iq - jk + AT_KEYS - 1]));
-        sv[kb * 4 + e] = v;
-        mx = fmaxf(mx, v);
-      }
+      for (int e = 0; e < 4; ++e) sv[kb * 4 + e] = __builtin_fmaf(s[kb][e], p.scale, pos[kb * 4 + e]);
+    if (j0 + AT_KEYS > len) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sv[k] = j0 + (k >> 2) * 16 + g * 4 + (k & 3) < len ? sv[k] : -INFINITY;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mx = fmaxf(mx, sv[k]);
     mx = xor32_max(xor16_max(mx));
-    const float alpha = __expf(m - mx);
+    const float alpha = __builtin_amdgcn_exp2f((m - mx) * L2E), nb = -mx * L2E;
     m = mx;
     float rs = 0.f;
     v8bf pb;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const float e = __expf(sv[k] - mx);
+      const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[k], L2E, nb));
       rs += e;
       pb[k] = (__bf16)e;
     }
@@ -360,7 +418,29 @@ relpos_attention_kernel(const AttnArgs p) {
       const v8bf va = __builtin_bit_cast(v8bf, make_uint4(lo.x, lo.y, hi.x, hi.y));
       o[ob] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[ob], 0, 0, 0);
     }
-    __syncthreads();  // every wave is done with the key and value tiles
+  };
+
+  fetch(0);
+  if constexpr (S::NBUF == 2) {
+    // tile t computes from buffer t & 1 while tile t + 1's data goes to the other one; the barrier after each tile
+    // publishes the next tile and retires the reads of this one
+    stash(0, sK0, sV0);
+    __syncthreads();
+    for (int j0 = 0, t = 0; j0 < len; j0 += AT_KEYS, ++t) {
+      const bool more = j0 + AT_KEYS < len;
+      if (more) fetch(j0 + AT_KEYS);
+      key_tile(j0, sK0 + (t & 1) * S::K_ELEMS, sV0 + (t & 1) * S::V_ELEMS);
+      if (more) stash(j0 + AT_KEYS, sK0 + ((t + 1) & 1) * S::K_ELEMS, sV0 + ((t + 1) & 1) * S::V_ELEMS);
+      __syncthreads();
+    }
+  } else {
+    for (int j0 = 0; j0 < len; j0 += AT_KEYS) {
+      stash(j0, sK0, sV0);
+      __syncthreads();
+      if (j0 + AT_KEYS < len) fetch(j0 + AT_KEYS);
+      key_tile(j0, sK0, sV0);
+      __syncthreads();  // every wave is done with the key and value tiles
+    }
   }
 
   if (!qvalid) return;
