@@ -371,13 +371,24 @@ relpos_attention_kernel(const AttnArgs p) {
       *reinterpret_cast<uint2*>(sPw + iq * AT_PW + pb * 16 + g * 4) = u;
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's position rows, written by other lanes
-    // the 8 position scores of this lane, read together (the addresses lie inside the wave's buffer for every key;
-    // the empty asm keeps the compiler from moving each read under the key mask, one after another)
+    // the 8 position scores of this lane, read together: key k = kb·16 + 4g + e sits at element
+    // iq·(AT_PW + 1) + 31 - k of the wave's buffer, inside it for every key, so no read waits under the key mask.
+    // Eight half-word reads from one base, written out so that the compiler neither fuses neighbours into misaligned
+    // wider reads nor moves each read under the mask, one after another.
     float pos[8];
+    {
+      const uint32_t a = (uint32_t)reinterpret_cast<uintptr_t>(sPw + iq * AT_PW + iq + AT_KEYS - 1 - g * 4 - 19);
+      uint32_t r[8];
+      asm volatile(
+          "ds_read_u16 %0, %8 offset:38\n\tds_read_u16 %1, %8 offset:36\n\tds_read_u16 %2, %8 offset:34\n\t"
+          "ds_read_u16 %3, %8 offset:32\n\tds_read_u16 %4, %8 offset:6\n\tds_read_u16 %5, %8 offset:4\n\t"
+          "ds_read_u16 %6, %8 offset:2\n\tds_read_u16 %7, %8\n\ts_waitcnt lgkmcnt(0)"
+          : "=v"(r[0]), "=v"(r[1]), "=v"(r[2]), "=v"(r[3]), "=v"(r[4]), "=v"(r[5]), "=v"(r[6]), "=v"(r[7])
+          : "v"(a)
+          : "memory");
 #pragma unroll
-    for (int k = 0; k < 8; ++k) pos[k] = bf2f(sPw[iq * AT_PW + iq - ((k >> 2) * 16 + g * 4 + (k & 3)) + AT_KEYS - 1]);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) asm volatile("" : "+v"(pos[k]));
+      for (int k = 0; k < 8; ++k) pos[k] = __uint_as_float(r[k] << 16);
+    }
 
     // scores (masked past the sequence in the last tile); online softmax per query (the 4 lane groups hold its
     // 32 keys). exp(v - mx) is taken as exp2(v log2 e - mx log2 e).
