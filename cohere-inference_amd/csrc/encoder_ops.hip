@@ -16,73 +16,70 @@
 namespace {
 
 // ---- depthwise convolution + BatchNorm + SiLU --------------------------------------------------------------------------
-// One workgroup holds DW_ROWS consecutive packed rows; each thread owns 8 channels, with their 9 taps, bias and
-// BatchNorm affine in registers and the DW_ROWS + 8 input rows it needs loaded once (16-byte loads). A tap reads
-// frame row + k - 4 only inside the row's own sequence [lo, hi) (zero padding at both ends of every sequence).
-// Per channel: acc = fmaf chain over the taps from the conv bias; a = bf16(acc); a = bf16(fmaf(a, bn_scale,
-// bn_shift)); y = bf16(a * sigmoid(a)). Q8 quantizes each output row with one scale (absmax / 127) instead of
-// storing bf16.
-constexpr int DW_K = 9, DW_PAD = 4, DW_ROWS = 8;
+// One workgroup holds DW_ROWS consecutive packed rows; each thread owns DW_CH = 4 channels, with their 9 taps, bias
+// and BatchNorm affine in registers and the DW_ROWS + 8 input rows it needs loaded once (8-byte loads). Small
+// per-thread state keeps four waves per SIMD and many workgroups in flight: the kernel is latency-bound, its bytes
+// are few. A tap reads frame row + k - 4 only inside the row's own sequence [lo, hi) (zero padding at both ends of
+// every sequence). Per channel: acc = fmaf chain over the taps from the conv bias; a = bf16(acc);
+// a = bf16(fmaf(a, bn_scale, bn_shift)); y = bf16(a * sigmoid(a)). Q8 quantizes each output row with one scale
+// (absmax / 127) instead of storing bf16.
+constexpr int DW_K = 9, DW_PAD = 4, DW_ROWS = 4, DW_CH = 4, DW_MAXW = 8;
 
 DEVI float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 DEVI float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 template <bool Q8>
-__global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict__ x, const float* __restrict__ w,
-                                                     const float* __restrict__ cb, const float* __restrict__ bn_scale,
-                                                     const float* __restrict__ bn_shift,
-                                                     const int32_t* __restrict__ seq_lo,
-                                                     const int32_t* __restrict__ seq_hi, uint16_t* __restrict__ y,
-                                                     int8_t* __restrict__ q, float* __restrict__ qs, int rows, int C) {
-  __shared__ float red[4][DW_ROWS];
-  const int tid = threadIdx.x, c = tid * 8, r0 = blockIdx.x * DW_ROWS;
+__global__ void __launch_bounds__(64 * DW_MAXW) dwconv_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ w, const float* __restrict__ cb,
+    const float* __restrict__ bn_scale, const float* __restrict__ bn_shift, const int32_t* __restrict__ seq_lo,
+    const int32_t* __restrict__ seq_hi, uint16_t* __restrict__ y, int8_t* __restrict__ q, float* __restrict__ qs,
+    int rows, int C) {
+  __shared__ float red[DW_MAXW][DW_ROWS];
+  const int tid = threadIdx.x, c = tid * DW_CH, r0 = blockIdx.x * DW_ROWS;
   const bool active = c < C;
-  uint4 in[DW_ROWS + DW_K - 1];
-  // a thread's 8 channels x 9 taps are 72 consecutive floats of the (C, 9) layout: 18 16-byte loads
-  float wk[8][DW_K], bias[8], sc[8], sh[8];
+  uint2 in[DW_ROWS + DW_K - 1];
+  // a thread's 4 channels x 9 taps are 36 consecutive floats of the (C, 9) layout: 9 16-byte loads
+  float wk[DW_CH][DW_K], bias[DW_CH], sc[DW_CH], sh[DW_CH];
   if (active) {
 #pragma unroll
     for (int i = 0; i < DW_ROWS + DW_K - 1; ++i) {
       const int gr = r0 - DW_PAD + i;
-      in[i] = gr >= 0 && gr < rows ? *reinterpret_cast<const uint4*>(x + (int64_t)gr * C + c) : make_uint4(0, 0, 0, 0);
+      in[i] = gr >= 0 && gr < rows ? *reinterpret_cast<const uint2*>(x + (int64_t)gr * C + c) : make_uint2(0, 0);
     }
     float* wf = &wk[0][0];
 #pragma unroll
-    for (int v = 0; v < 8 * DW_K / 4; ++v)
+    for (int v = 0; v < DW_CH * DW_K / 4; ++v)
       *reinterpret_cast<float4*>(wf + 4 * v) = *reinterpret_cast<const float4*>(w + (int64_t)c * DW_K + 4 * v);
-#pragma unroll
-    for (int j = 0; j < 8; j += 4) {
-      *reinterpret_cast<float4*>(bias + j) = *reinterpret_cast<const float4*>(cb + c + j);
-      *reinterpret_cast<float4*>(sc + j) = *reinterpret_cast<const float4*>(bn_scale + c + j);
-      *reinterpret_cast<float4*>(sh + j) = *reinterpret_cast<const float4*>(bn_shift + c + j);
-    }
+    *reinterpret_cast<float4*>(bias) = *reinterpret_cast<const float4*>(cb + c);
+    *reinterpret_cast<float4*>(sc) = *reinterpret_cast<const float4*>(bn_scale + c);
+    *reinterpret_cast<float4*>(sh) = *reinterpret_cast<const float4*>(bn_shift + c);
   }
-  float out[DW_ROWS][8];
+  float out[DW_ROWS][DW_CH];
   float mx[DW_ROWS];
 #pragma unroll
   for (int r = 0; r < DW_ROWS; ++r) {
     const int row = r0 + r;
     mx[r] = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) out[r][j] = 0.f;
+    for (int j = 0; j < DW_CH; ++j) out[r][j] = 0.f;
     if (!active || row >= rows) continue;
     const int lo = seq_lo[row], hi = seq_hi[row];
-    float acc[8];
+    float acc[DW_CH];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = bias[j];
+    for (int j = 0; j < DW_CH; ++j) acc[j] = bias[j];
 #pragma unroll
     for (int k = 0; k < DW_K; ++k) {
       const int src = row + k - DW_PAD;
       if (src < lo || src >= hi) continue;
-      const uint32_t e[4] = {in[r + k].x, in[r + k].y, in[r + k].z, in[r + k].w};
+      const uint32_t e[2] = {in[r + k].x, in[r + k].y};
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < DW_CH; ++j) {
         const float xv = j & 1 ? bf_hi(e[j >> 1]) : bf_lo(e[j >> 1]);
         acc[j] = __builtin_fmaf(xv, wk[j][k], acc[j]);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < DW_CH; ++j) {
       float a = round_bf(acc[j]);
       a = round_bf(__builtin_fmaf(a, sc[j], sh[j]));
       out[r][j] = round_bf(a * sigmoid_fast(a));
@@ -95,12 +92,8 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
     for (int r = 0; r < DW_ROWS; ++r) {
       const int row = r0 + r;
       if (row >= rows) break;
-      uint4 u;
-      u.x = pack_bf2(out[r][0], out[r][1]);
-      u.y = pack_bf2(out[r][2], out[r][3]);
-      u.z = pack_bf2(out[r][4], out[r][5]);
-      u.w = pack_bf2(out[r][6], out[r][7]);
-      *reinterpret_cast<uint4*>(y + (int64_t)row * C + c) = u;
+      *reinterpret_cast<uint2*>(y + (int64_t)row * C + c) =
+          make_uint2(pack_bf2(out[r][0], out[r][1]), pack_bf2(out[r][2], out[r][3]));
     }
   } else {
     const int wv = tid >> 6, nw = blockDim.x >> 6;
@@ -118,13 +111,13 @@ __global__ void __launch_bounds__(256) dwconv_kernel(const uint16_t* __restrict_
       for (int k = 1; k < nw; ++k) m = fmaxf(m, red[k][r]);
       const float s = m > 0.f ? m / 127.f : 1.f, inv = 1.f / s;
       if (active) {
-        uint32_t v[2] = {0, 0};
+        uint32_t v = 0;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
+        for (int k = 0; k < DW_CH; ++k) {
           const int qi = (int)rintf(fminf(fmaxf(out[r][k] * inv, -127.f), 127.f));
-          v[k >> 2] |= (uint32_t)(qi & 0xff) << ((k & 3) * 8);
+          v |= (uint32_t)(qi & 0xff) << (k * 8);
         }
-        *reinterpret_cast<uint2*>(q + (int64_t)row * C + c) = make_uint2(v[0], v[1]);
+        *reinterpret_cast<uint32_t*>(q + (int64_t)row * C + c) = v;
       }
       if (tid == 0) qs[row] = s;
     }
@@ -481,7 +474,7 @@ int dwconv_entry(const uint16_t* x, const float* w, const float* cb, const float
   COHERE_REQUIRE(Q8 ? (q && qs && (reinterpret_cast<uintptr_t>(q) & 7) == 0) : (y && al16(y)),
                  nm + ": bad output pointer");
   if (rows == 0) return 0;
-  const int threads = (int)((C / 8 + 63) / 64 * 64);
+  const int threads = (int)((C / DW_CH + 63) / 64 * 64);
   const int grid = (int)((rows + DW_ROWS - 1) / DW_ROWS);
   dwconv_kernel<Q8><<<grid, threads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
       x, w, cb, bn_scale, bn_shift, seq_lo, seq_hi, y, q, qs, (int)rows, (int)C);
