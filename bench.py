@@ -428,9 +428,24 @@ def block_extra(dev, replays=20):
         graph.replay()
     ms = time_graph(graph, replays)
     gemm_ops = 2.0 * M * D * (4 * F + 3 * D + D + 2 * D + D)  # FF1/FF2 W1+W2, QKV, O, PW1 (GLU), PW2
+    # the block's relative-position attention on its own (random q, k, v and table): 20 launches in a graph
+    from kernels.cuda_ext import ext
+
+    heads, hd = 16, D // 16
+    qkv = torch.randn(M, 3 * D, generator=g).to(torch.bfloat16).to(dev)
+    rk = torch.randn(2 * 375 - 1 + 64, D, generator=g).to(torch.bfloat16).to(dev)  # the kernel reads 63 rows past
+    bu, bv = (0.1 * torch.randn(heads, hd, generator=g)).to(torch.bfloat16).to(dev), \
+        (0.1 * torch.randn(heads, hd, generator=g)).to(torch.bfloat16).to(dev)
+    att = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    ga = graph_of(lambda: ext.relpos_attention(qkv, rk, bu, bv, meta["tiles"], 374, 375, hd ** -0.5, att), 20)
+    for _ in range(3):
+        ga.replay()
+    att_us = min(time_graph(ga, replays) for _ in range(3)) / 20 * 1e3  # best of 3: the first runs while clocks rise
+    att_flops = 3 * 2.0 * 8 * heads * 375 * 375 * hd  # content scores, position scores, probabilities x values
     return {"what": "config 2: one FastConformer block (d 1280, 16 heads of 80, FFN 5120 with both linears 2:4, conv module), "
                     "all linears W8A8, 8 x 375 packed frames, native layer loop (15 launches) in a HIP graph",
             "ms_per_block": round(ms, 4), "gemm_ops": gemm_ops,
+            "attention_us": round(att_us, 2), "attention_TFLOPs": round(att_flops / (att_us * 1e-6) / 1e12, 1),
             "gemm_TOPS_over_block": round(gemm_ops / (ms * 1e-3) / 1e12, 1),
             "encoder_layers_audio_sec_per_sec": round(8 * 30.0 / (24 * ms * 1e-3), 1),
             "note": "audio-sec/sec of the 24 encoder layers alone (8 clips x 30 s through 24 such blocks); no "
