@@ -111,7 +111,7 @@ def _attention_case(lengths, H, D, seed, max_len=512):
 
 
 @pytest.mark.parametrize("H,D,lengths", [(8, 160, [375, 200, 64, 1, 97]), (16, 80, [375, 33, 130]),
-                                         (16, 80, [512]), (8, 160, [2, 65])])
+                                         (16, 80, [512]), (8, 160, [2, 65]), (16, 80, [1, 32, 31, 64, 96, 33])])
 def test_relpos_attention(gpu, H, D, lengths):
     from kernels.fast_encoder import metadata
 
