@@ -76,9 +76,10 @@ def _dwconv_inputs(lengths, C=1280, seed=22):
     return x, w, cb, sc, sh, lo, hi
 
 
-@pytest.mark.parametrize("lengths", [[375, 200, 1, 64, 97], [3], [8, 9]])
-def test_dwconv_bn_silu_bf16_and_q8(gpu, lengths):
-    x, w, cb, sc, sh, lo, hi = _dwconv_inputs(lengths)
+@pytest.mark.parametrize("lengths,C", [([375, 200, 1, 64, 97], 1280), ([3], 1280), ([8, 9], 1280),
+                                      ([5, 130, 2], 2048), ([7, 1, 40], 8), ([33, 4], 520)])
+def test_dwconv_bn_silu_bf16_and_q8(gpu, lengths, C):
+    x, w, cb, sc, sh, lo, hi = _dwconv_inputs(lengths, C=C)
     d = lambda t: t.to(gpu).contiguous()  # noqa: E731
     lo_d, hi_d = d(torch.from_numpy(lo)), d(torch.from_numpy(hi))
     y = torch.empty_like(d(x))
