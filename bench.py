@@ -53,8 +53,10 @@ def log(msg: str) -> None:
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # about 0.1 s each at config 1: the GPU's clocks rise over the first tens of milliseconds of sustained work
+    # (49.6 us per step after 20 warm-up steps, 44.6 after 2000), and a serving GPU runs warm
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=2000)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the two rocprofv3 --pmc passes for the traffic")
@@ -104,6 +106,13 @@ def graph_of(fn, reps):
     with torch.cuda.graph(g):
         for _ in range(reps):
             fn()
+    return g
+
+
+def warm(g, replays=50):
+    """Replays g untimed (the GPU's clocks rise under sustained work) and returns it."""
+    for _ in range(replays):
+        g.replay()
     return g
 
 
@@ -424,9 +433,7 @@ def block_extra(dev, replays=20):
     g = torch.Generator().manual_seed(2)
     x = torch.randn(M, D, generator=g).to(torch.bfloat16).to(dev)
     graph = graph_of(lambda: layers(x, lengths, meta), 1)
-    for _ in range(3):
-        graph.replay()
-    ms = time_graph(graph, replays)
+    ms = time_graph(warm(graph, 30), replays)
     gemm_ops = 2.0 * M * D * (4 * F + 3 * D + D + 2 * D + D)  # FF1/FF2 W1+W2, QKV, O, PW1 (GLU), PW2
     # the block's relative-position attention on its own (random q, k, v and table): 20 launches in a graph
     from kernels.cuda_ext import ext
@@ -438,9 +445,7 @@ def block_extra(dev, replays=20):
         (0.1 * torch.randn(heads, hd, generator=g)).to(torch.bfloat16).to(dev)
     att = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
     ga = graph_of(lambda: ext.relpos_attention(qkv, rk, bu, bv, meta["tiles"], 374, 375, hd ** -0.5, att), 20)
-    for _ in range(3):
-        ga.replay()
-    att_us = min(time_graph(ga, replays) for _ in range(3)) / 20 * 1e3  # best of 3: the first runs while clocks rise
+    att_us = time_graph(warm(ga), replays) / 20 * 1e3
     att_flops = 3 * 2.0 * 8 * heads * 375 * 375 * hd  # content scores, position scores, probabilities x values
     return {"what": "config 2: one FastConformer block (d 1280, 16 heads of 80, FFN 5120 with both linears 2:4, conv module), "
                     "all linears W8A8, 8 x 375 packed frames, native layer loop (15 launches) in a HIP graph",
@@ -743,8 +748,8 @@ def main():
         log("dominant kernel")
         # each kernel of the step alone: the dominant one's duration prices the roofline
         reps = 20
-        ms_up = time_graph(graph_of(up, reps), 10) / reps
-        ms_dn = time_graph(graph_of(down, reps), 10) / reps
+        ms_up = time_graph(warm(graph_of(up, reps)), 10) / reps
+        ms_dn = time_graph(warm(graph_of(down, reps)), 10) / reps
         dom = ("gemm_sp up 3000x5120x1280", ms_up, ops_up) if ms_up >= ms_dn else \
               ("gemm_sp down 3000x1280x5120", ms_dn, ops_dn)
         achieved = dom[2] / (dom[1] * 1e-3)
@@ -787,7 +792,7 @@ def main():
         def dense():
             d["up_d"](d["xq"], d["xs"], EPI_BIAS, out=up_out)
 
-        ms_d = time_graph(graph_of(dense, 20), 10) / 20
+        ms_d = time_graph(warm(graph_of(dense, 20)), 10) / 20
         result["dense_config0"] = {"what": "dense W8A8 3000x5120x1280, bias epilogue (config 0)",
                                    "ms": round(ms_d, 5), "TOPS": round(ops_up / (ms_d * 1e-3) / 1e12, 1),
                                    "frac_of_dense_peak": round(ops_up / (ms_d * 1e-3) / PEAK_INT8_DENSE, 4)}
@@ -797,7 +802,7 @@ def main():
         for name, (mm, nn, kk) in (("config0", (M, F, D)), ("down", (M, D, F))):
             xa = torch.randint(-127, 128, (mm, kk), dtype=torch.int8, device=dev)
             wa = torch.randint(-127, 128, (nn, kk), dtype=torch.int8, device=dev)
-            ms_v = time_graph(graph_of(lambda: torch._int_mm(xa, wa.t()), 20), 10) / 20
+            ms_v = time_graph(warm(graph_of(lambda: torch._int_mm(xa, wa.t()), 20)), 10) / 20
             vendor[name] = {"shape": [mm, nn, kk], "ms": round(ms_v, 5),
                             "TOPS": round(2 * mm * nn * kk / (ms_v * 1e-3) / 1e12, 1)}
             del xa, wa
