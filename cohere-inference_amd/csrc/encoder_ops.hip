@@ -427,7 +427,9 @@ relpos_attention_kernel(const AttnArgs p) {
   fetch(0);
   if constexpr (S::NBUF == 2) {
     // tile t computes from buffer t & 1 while tile t + 1's data goes to the other one; the barrier after each tile
-    // publishes the next tile and retires the reads of this one
+    // publishes the next tile and retires the reads of this one. The table rows tile t + 1 adds to the ring
+    // (distances q0 - j0 - 63 .. q0 - j0 - 32) are not among the 96 that tile t reads (q0 - j0 - 31 .. q0 - j0 + 64),
+    // modulo the ring's 128, so they are written while tile t computes
     stash(0, sK0, sV0);
     __syncthreads();
     for (int j0 = 0, t = 0; j0 < len; j0 += AT_KEYS, ++t) {
