@@ -11,7 +11,6 @@
 #include "common.h"
 
 #include <string>
-#include <type_traits>
 
 namespace {
 
