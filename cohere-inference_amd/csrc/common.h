@@ -32,6 +32,18 @@ DEVI uint32_t pack_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// four values as int8, rint(clamp(f * inv, -127, 127)) each, packed low byte first, for inv = 1 / (m / 127) where m
+// is at least the largest |f| of the values quantized with it: then |f * inv| <= 127 (1 + 4 ulp) < 127.5 and the
+// clamp never acts. Adding 1.5 * 2^23 to the rounded product rounds it to an integer, half to even like rintf, and
+// leaves that integer k in the low mantissa bits (0x4B400000 + k), so the sum's low byte is k's two's-complement
+// byte; two byte permutes pack the four (selector byte 0x0c gives a zero byte).
+DEVI uint32_t q8x4(float a, float b, float c, float d, float inv) {
+  const uint32_t ba = __float_as_uint(a * inv + 12582912.f), bb = __float_as_uint(b * inv + 12582912.f),
+                 bc = __float_as_uint(c * inv + 12582912.f), bd = __float_as_uint(d * inv + 12582912.f);
+  return __builtin_amdgcn_perm(__builtin_amdgcn_perm(bd, bc, 0x0c0c0400u), __builtin_amdgcn_perm(bb, ba, 0x0c0c0400u),
+                               0x05040100u);
+}
+
 // logistic for the activation epilogues (hardware exp and reciprocal); their results are rounded to bf16 or int8
 // right after, far coarser than these approximations
 DEVI float sigmoid_fast(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }

@@ -135,13 +135,9 @@ DEVI void store16_q8(const float (&f)[16], int8_t* dst, float* scale, int gl) {
   for (int k = 0; k < 16; ++k) mx = fmaxf(mx, fabsf(f[k]));
   mx = group_max(mx);
   const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
-  uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int q = (int)rintf(fminf(fmaxf(f[k] * inv, -127.f), 127.f));
-    w[k >> 2] |= (uint32_t)(q & 0xff) << ((k & 3) * 8);
-  }
-  *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  *reinterpret_cast<uint4*>(dst) = make_uint4(q8x4(f[0], f[1], f[2], f[3], inv), q8x4(f[4], f[5], f[6], f[7], inv),
+                                               q8x4(f[8], f[9], f[10], f[11], inv),
+                                               q8x4(f[12], f[13], f[14], f[15], inv));
   if (gl == 0) *scale = sc;
 }
 
@@ -623,13 +619,8 @@ __global__ void __launch_bounds__(256) dec_scatter_kv_kernel(const uint16_t* __r
     mx = row16_max(mx);
     if (!live) return;
     const float sc = mx > 0.f ? mx / 127.f : 1.f, inv = 1.f / sc;
-    uint32_t q[2] = {0, 0};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int qi = (int)rintf(fminf(fmaxf(f[k] * inv, -127.f), 127.f));
-      q[k >> 2] |= (uint32_t)(qi & 0xff) << ((k & 3) * 8);
-    }
-    *reinterpret_cast<uint2*>((kvi ? cv8 : ck8) + vec * HD + d8 * 8) = make_uint2(q[0], q[1]);
+    *reinterpret_cast<uint2*>((kvi ? cv8 : ck8) + vec * HD + d8 * 8) =
+        make_uint2(q8x4(f[0], f[1], f[2], f[3], inv), q8x4(f[4], f[5], f[6], f[7], inv));
     if (d8 == 0) (kvi ? cvs : cks)[vec] = sc;
   }
 }

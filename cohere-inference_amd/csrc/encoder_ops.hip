@@ -110,13 +110,8 @@ __global__ void __launch_bounds__(64 * DW_MAXW) dwconv_kernel(
       for (int k = 1; k < nw; ++k) m = fmaxf(m, red[k][r]);
       const float s = m > 0.f ? m / 127.f : 1.f, inv = 1.f / s;
       if (active) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int k = 0; k < DW_CH; ++k) {
-          const int qi = (int)rintf(fminf(fmaxf(out[r][k] * inv, -127.f), 127.f));
-          v |= (uint32_t)(qi & 0xff) << (k * 8);
-        }
-        *reinterpret_cast<uint32_t*>(q + (int64_t)row * C + c) = v;
+        static_assert(DW_CH == 4, "one q8x4 per row");
+        *reinterpret_cast<uint32_t*>(q + (int64_t)row * C + c) = q8x4(out[r][0], out[r][1], out[r][2], out[r][3], inv);
       }
       if (tid == 0) qs[row] = s;
     }

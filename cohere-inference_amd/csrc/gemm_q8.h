@@ -722,17 +722,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
           const float inv = ginv[gi];
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
-            // rint(clamp(u * inv, -127, 127)) as int8: |u| <= the group's maximum mx and inv = 1 / bf(mx / 127), so
-            // |u * inv| <= 127 (1 + 4 ulp) < 127.5 and the clamp never acts. Adding 1.5 * 2^23 to the rounded
-            // product rounds it to an integer, half to even like rintf, and leaves that integer in the low mantissa
-            // bits (0x4B400000 + k): the low byte of the sum is k's two's-complement byte. Two byte permutes pack
-            // the four bytes (selector 0x0c gives a zero byte).
-            uint32_t b[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-              b[r] = __float_as_uint(__int_as_float(acc[j][i][4 * q + r]) * inv + 12582912.f);
-            const uint32_t o = __builtin_amdgcn_perm(__builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u),
-                                                     __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), 0x05040100u);
+            const uint32_t o = q8x4(__int_as_float(acc[j][i][4 * q]), __int_as_float(acc[j][i][4 * q + 1]),
+                                    __int_as_float(acc[j][i][4 * q + 2]), __int_as_float(acc[j][i][4 * q + 3]), inv);
             *reinterpret_cast<uint32_t*>(so + slot(rl, chan(j, q))) = o;
           }
           if (lhi == 0 && cb == g0 && m < M) p.qs[(int64_t)m * p.ldqs + (n0 + cb * MS) / p.qgroup] = gsc[gi];

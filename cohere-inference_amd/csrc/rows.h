@@ -40,13 +40,8 @@ DEVI void store_q8(const Row<VEC>& r, int cols, int lane, int8_t* q, float* scal
   for (int i = 0; i < VEC; ++i) {
     const int c = (i * 64 + lane) * 8;
     if (c >= cols) continue;
-    uint32_t w[2] = {0, 0};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int v = (int)rintf(fminf(fmaxf(r.v[i][k] * inv, -127.f), 127.f));
-      w[k >> 2] |= (uint32_t)(v & 0xff) << ((k & 3) * 8);
-    }
-    *reinterpret_cast<uint2*>(q + c) = make_uint2(w[0], w[1]);
+    const float* f = r.v[i];
+    *reinterpret_cast<uint2*>(q + c) = make_uint2(q8x4(f[0], f[1], f[2], f[3], inv), q8x4(f[4], f[5], f[6], f[7], inv));
   }
   if (lane == 0) *scale = s;
 }
