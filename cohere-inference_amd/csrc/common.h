@@ -26,6 +26,16 @@ DEVI uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 DEVI float round_bf(float f) { return bf2f(f2bf(f)); }
 
+// round_bf in one instruction: the conversion packs bf16(0) below bf16(f), which is bf16(f)'s fp32 bit pattern (the
+// same packing written in C becomes the conversion plus a byte permute). Only for an f that an ordinary VALU
+// instruction wrote: the compiler puts no wait states before inline assembly, and reading a matrix instruction's
+// result (or a transcendental's) that early gives stale values.
+DEVI float round_bf_valu(float f) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(f));
+  return r;
+}
+
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 DEVI uint32_t pack_bf2(float lo, float hi) {
   const v2bf v = {(__bf16)lo, (__bf16)hi};
@@ -139,6 +149,17 @@ DEVI float xor32_sum(float v) {
 DEVI float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// the same two maxima for non-negative values (not NaN): compared as unsigned bit patterns, whose order is theirs,
+// which takes one integer maximum where fmaxf first quiets both operands
+DEVI float xor16_max_pos(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0] > r[1] ? r[0] : r[1]);
+}
+DEVI float xor32_max_pos(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0] > r[1] ? r[0] : r[1]);
 }
 
 DEVI float wave_max_xor(float v, int width) {

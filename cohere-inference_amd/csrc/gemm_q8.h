@@ -658,27 +658,22 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       for (int j = 0; j < NI; ++j)
 #pragma unroll
         for (int i = 0; i < MI; ++i) {
-          // the bf16 roundings two values per conversion; the maximum taken before the second rounding and rounded
-          // once at the end (bf16 rounding is monotonic and symmetric, so that is the maximum of the rounded |u|)
+          // u = bf16(silu(bf16(v))) as fp32 bits in the accumulator; the maximum of |u| over the lane's block
           float mx = 0.f;
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
             float v[4];
             dequant(j, i, q, v);
 #pragma unroll
-            for (int r = 0; r < 4; r += 2) {
-              const uint32_t tp = pack_bf2(v[r], v[r + 1]);
-              const float t0 = __uint_as_float(tp << 16), t1 = __uint_as_float(tp & 0xffff0000u);
-              const float s0 = t0 * sigmoid_fast(t0), s1 = t1 * sigmoid_fast(t1);
-              mx = fmaxf(mx, fmaxf(fabsf(s0), fabsf(s1)));
-              const uint32_t up = pack_bf2(s0, s1);
-              acc[j][i][4 * q + r] = (int)(up << 16);
-              acc[j][i][4 * q + r + 1] = (int)(up & 0xffff0000u);
+            for (int r = 0; r < 4; ++r) {
+              const float t = round_bf_valu(v[r]);  // v: an fma's result
+              const float u = round_bf_valu(t * sigmoid_fast(t));
+              mx = fmaxf(mx, fabsf(u));
+              acc[j][i][4 * q + r] = __float_as_int(u);
             }
           }
-          mx = round_bf(mx);
-          if constexpr (MS == 16) mx = xor32_max(xor16_max(mx));
-          else mx = xor32_max(mx);
+          if constexpr (MS == 16) mx = xor32_max_pos(xor16_max_pos(mx));
+          else mx = xor32_max_pos(mx);
           if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
         }
       __syncthreads();
