@@ -34,7 +34,11 @@ __global__ void __launch_bounds__(64 * DW_MAXW) dwconv_kernel(
     const int32_t* __restrict__ seq_hi, uint16_t* __restrict__ y, int8_t* __restrict__ q, float* __restrict__ qs,
     int rows, int C) {
   __shared__ float red[DW_MAXW][DW_ROWS];
-  const int tid = threadIdx.x, c = tid * DW_CH, r0 = blockIdx.x * DW_ROWS;
+  // XCD-aware order: workgroup b runs on XCD b % 8, so each XCD takes one contiguous run of row blocks and the 8
+  // halo rows a block shares with its neighbours are fetched into that XCD's L2 once
+  const int nb = (int)gridDim.x, xcd = (int)blockIdx.x % 8;
+  const int blk = xcd * (nb / 8) + min(xcd, nb % 8) + (int)blockIdx.x / 8;
+  const int tid = threadIdx.x, c = tid * DW_CH, r0 = blk * DW_ROWS;
   const bool active = c < C;
   uint2 in[DW_ROWS + DW_K - 1];
   // a thread's 4 channels x 9 taps are 36 consecutive floats of the (C, 9) layout: 9 16-byte loads
