@@ -70,7 +70,9 @@ struct GemmArgs {
 // 128-wide K stage kt, one contiguous record of TILED_REC bytes at (rb * K/128 + kt) * TILED_REC: 1024 bytes of kept
 // values, 16-byte chunk i holding row i / 4's logical chunk (i % 4) ^ ((i / 8) % 4) of its 64 kept bytes of the stage
 // (the LDS swizzle, so a DMA lane's 16 bytes land where the fragment reads expect them), then 256 bytes of
-// selectors, row r's four words of the stage at 16 r. Every 1 KB DMA instruction then reads one contiguous kilobyte
+// selectors, row r's four words of the stage at 16 r, with words 0-1 and 2-3 swapped in rows 8-15 (a selector read
+// of 32 lanes -- rows 0-15, two words each -- then touches 32 distinct banks: unswizzled, rows r and r + 8 share
+// banks). Every 1 KB DMA instruction then reads one contiguous kilobyte
 // (row-major weights give 16 rows x 64 bytes: half of each 128-byte line), and a stage's selectors of 16 rows one
 // 256-byte run (row-major: 16 bytes of each of 16 lines).
 constexpr int TILED_REC = 1280;
@@ -353,6 +355,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       // (h = lane/32). A (kept weights): compressed chunk h / 2s + h, and the selector word of the same 32 K.
       const int c0 = MS == 16 ? lhi : 4 * s + lhi, c1 = MS == 16 ? 4 + lhi : 4 * s + 2 + lhi;
       const int ca = MS == 16 ? lhi : 2 * s + lhi;
+      // the stage-tiled layout stores rows 8-15 of each 16-row block with selector words 0-1 and 2-3 swapped
+      const int cs = ca ^ (p.tiled ? (lrow & 8) >> 2 : 0);
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int r = wm * TM + i * MS + lrow;
@@ -364,7 +368,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       for (int j = 0; j < NI; ++j) {
         const int r = wn * TN + j * MS + lrow;
         F.aw[j] = *reinterpret_cast<const v4i*>(ws + sw64(r, ca));
-        F.ix[j] = *reinterpret_cast<const int*>(es + r * 16 + ca * 4);
+        F.ix[j] = *reinterpret_cast<const int*>(es + r * 16 + cs * 4);
       }
     }
   };
@@ -588,14 +592,16 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
                   EPI == EPI_CONV_RELU) {
       // the tile's bf16 results are staged in LDS (over the pipeline buffers, free now) and written out as whole
       // rows: each 16-byte store then covers 8 consecutive channels of one row, where the lanes' own results would
-      // give 16 rows x 8 bytes per instruction. Rows are stored with their 16-byte chunks XOR-swizzled by row, so
-      // both the 8-byte stage writes (16 rows, one column) and the row reads are free of bank conflicts.
+      // give 16 rows x 8 bytes per instruction. A row's 8-byte units (4 channels) are XOR-swizzled by the row's low
+      // four bits, so the stage writes (16 rows, one unit: 16 distinct bank pairs) are free of bank conflicts; a
+      // 16-byte row read then finds its chunk at cc ^ (g >> 1), its two halves swapped when g is odd.
       constexpr int OC = EPI == EPI_GLU ? BN / 2 : BN;  // output channels per tile row
       constexpr int CPR = OC / 8;                       // 16-byte chunks per row
+      constexpr int GM = (OC / 4 < 16 ? OC / 4 : 16) - 1;
       static_assert(BM * OC * 2 <= T::PIPE && (CPR & (CPR - 1)) == 0, "epilogue staging");
       char* so = smem;
       auto slot = [&](int row, int col) {  // byte offset of output column col (bf16) of tile row row
-        return row * (OC * 2) + ((((col >> 3) ^ row) & (CPR - 1)) << 4) + (col & 7) * 2;
+        return row * (OC * 2) + (((col >> 2) ^ (row & GM)) << 3) + (col & 3) * 2;
       };
       lds_barrier();  // every wave is done reading the pipeline buffers
 #pragma unroll
@@ -630,9 +636,10 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       lds_barrier();
       const int oc0 = EPI == EPI_GLU ? n0 / 2 : n0;
       for (int idx = tid; idx < BM * CPR; idx += NT) {
-        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl;
+        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl, g = rl & GM;
         if (m >= M) continue;
-        uint4 o = *reinterpret_cast<const uint4*>(so + slot(rl, cc * 8));
+        uint4 o = *reinterpret_cast<const uint4*>(so + rl * (OC * 2) + ((cc ^ (g >> 1)) << 4));
+        if (g & 1) o = make_uint4(o.z, o.w, o.x, o.y);
         if constexpr (EPI == EPI_RESID) {
           // out = bf16(alpha * bf16(v) + r); out may be r itself (this thread reads the chunk before writing it)
           const uint4 rv = *reinterpret_cast<const uint4*>(p.R + (int64_t)m * p.ldr + oc0 + cc * 8);
@@ -699,14 +706,16 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       }
       __syncthreads();
       // the int8 tile is staged in LDS past the tables and written out as whole rows (16-byte stores of 16
-      // consecutive channels, where the lanes' own values would be 4-byte stores, 16 rows per instruction); 16-byte
-      // chunks are XOR-swizzled by row, so the 4-byte stage writes (16 rows, one chunk) and the row reads are free of
-      // bank conflicts
+      // consecutive channels, where the lanes' own values would be 4-byte stores, 16 rows per instruction). A row's
+      // 4-byte units are XOR-swizzled by twice the row's low four bits, so the stage writes (16 rows at one unit,
+      // 16 rows at the next: 32 distinct banks) are free of bank conflicts; a 16-byte row read then finds its chunk
+      // at cc ^ (g >> 2), its two halves swapped when g & 2.
       constexpr int CPR = BN / 16;  // 16-byte chunks per tile row
       constexpr int TABLES = BM * (CB + 2 * BN / 64) * 4;
       static_assert(TABLES + BM * BN <= T::PIPE && (CPR & (CPR - 1)) == 0, "int8 staging");
       char* so = smem + TABLES;
-      auto slot = [&](int row, int col) { return row * BN + ((((col >> 4) ^ row) & (CPR - 1)) << 4) + (col & 15); };
+      auto swz = [&](int row) { return ((row & 15) << 1) & (BN / 4 - 1); };
+      auto slot = [&](int row, int col) { return row * BN + (((col >> 2) ^ swz(row)) << 2) + (col & 3); };
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int rl = tok(i), m = m0 + rl;
@@ -726,10 +735,11 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       }
       lds_barrier();
       for (int idx = tid; idx < BM * CPR; idx += NT) {
-        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl;
+        const int rl = idx / CPR, cc = idx % CPR, m = m0 + rl, g = swz(rl);
         if (m >= M) continue;
-        *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n0 + cc * 16) =
-            *reinterpret_cast<const uint4*>(so + slot(rl, cc * 16));
+        uint4 o = *reinterpret_cast<const uint4*>(so + rl * BN + ((cc ^ (g >> 2)) << 4));
+        if (g & 2) o = make_uint4(o.z, o.w, o.x, o.y);
+        *reinterpret_cast<uint4*>(reinterpret_cast<int8_t*>(p.C) + (int64_t)m * p.ldc + n0 + cc * 16) = o;
       }
     }
   }

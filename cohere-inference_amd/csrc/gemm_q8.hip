@@ -183,7 +183,10 @@ extern "C" int cohere_pack_24_tiled(const int8_t* wc, const int32_t* e, int64_t 
         const int c = (i % 4) ^ ((i / 8) % 4);
         std::memcpy(rec + 16 * i, wc + row * (K / 2) + kt * 64 + c * 16, 16);
       }
-      for (int r = 0; r < 16; ++r) std::memcpy(rec + 1024 + 16 * r, e + (rb * 16 + r) * (K / 32) + kt * 4, 16);
+      // row r's four selector words, words 0-1 and 2-3 swapped in rows 8-15 (see TILED_REC)
+      for (int r = 0; r < 16; ++r)
+        for (int w = 0; w < 4; ++w)
+          std::memcpy(rec + 1024 + 16 * r + 4 * (w ^ (r & 8 ? 2 : 0)), e + (rb * 16 + r) * (K / 32) + kt * 4 + w, 4);
     }
   return 0;
 }

@@ -78,7 +78,8 @@ def pack_24_tiled(kept: torch.Tensor, words: torch.Tensor) -> torch.Tensor:
     """compress_24's storage rearranged for the gfx950 sparse GEMM's loads (ext.gemm_sp_tiled; load time, on the
     tensors' device): uint8 (N/16, K/128, 1280), one record per block of 16 channels and 128-wide K stage -- the 64
     16-byte chunks of the block's kept values of the stage (chunk i: row i // 4, its chunk (i % 4) ^ ((i // 8) % 4),
-    the LDS swizzle applied ahead of time), then the 16 rows' four selector words of the stage. The same bytes as the
+    the LDS swizzle applied ahead of time), then the 16 rows' four selector words of the stage (in rows 8-15 words 0-1
+    and 2-3 swapped, so that the GEMM's selector reads from LDS are free of bank conflicts). The same bytes as the
     library's cohere_pack_24_tiled."""
     n, half = kept.shape
     assert kept.dtype == torch.int8 and words.dtype == torch.int32 and n % 16 == 0 and half % 64 == 0
@@ -87,5 +88,9 @@ def pack_24_tiled(kept: torch.Tensor, words: torch.Tensor) -> torch.Tensor:
     blocks = kept.view(n // 16, 16, kt, 4, 16).permute(0, 2, 1, 3, 4)  # (block, stage, row, chunk, 16 bytes)
     i = torch.arange(64, device=kept.device)
     chunks = blocks[:, :, i // 4, (i % 4) ^ ((i // 8) % 4), :].reshape(n // 16, kt, 1024)
-    sel = words.view(n // 16, 16, kt, 4).permute(0, 2, 1, 3).contiguous().view(torch.uint8).reshape(n // 16, kt, 256)
+    sel = words.view(n // 16, 16, kt, 4).permute(0, 2, 1, 3)  # (block, stage, row, word)
+    r = torch.arange(16, device=kept.device)[:, None]
+    w = torch.arange(4, device=kept.device)[None, :]
+    sel = sel[:, :, r, w ^ torch.where(r >= 8, 2, 0)]  # rows 8-15: words 0-1 and 2-3 swapped
+    sel = sel.contiguous().view(torch.uint8).reshape(n // 16, kt, 256)
     return torch.cat([chunks.view(torch.uint8), sel], dim=2).contiguous()

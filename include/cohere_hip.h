@@ -77,7 +77,7 @@ int cohere_gemm_sp_tiled(const int8_t* x, int64_t ldx, const float* sx, int64_t 
  * compress_24's kept values wc int8 [N, K/2] and selectors e int32 [N, K/32] into out, cohere_pack_24_tiled_bytes(N, K)
  * bytes (-1 unless N % 16 == 0 and K % 128 == 0). For each block of 16 channels and each 128-wide K stage, one
  * 1280-byte record: 64 chunks of 16 kept bytes (chunk i = row i/4's chunk (i%4) ^ ((i/8)%4) of the stage), then the
- * 16 rows' four selector words of the stage. */
+ * 16 rows' four selector words of the stage (rows 8-15 with words 0-1 and 2-3 swapped). */
 int64_t cohere_pack_24_tiled_bytes(int64_t N, int64_t K);
 int cohere_pack_24_tiled(const int8_t* wc, const int32_t* e, int64_t N, int64_t K, uint8_t* out);
 

@@ -148,7 +148,8 @@ def test_weight_quantizers_match_oracle():
 def test_pack_24_tiled_matches_c_abi_and_round_trips():
     """The stage-tiled 2:4 layout: kernels.sparse.pack_24_tiled (torch) and the library's cohere_pack_24_tiled (host
     loops) give the same bytes, and every record decodes back to compress_24's kept values and selectors through the
-    layout's own definition (chunk i = row i // 4, logical chunk (i % 4) ^ ((i // 8) % 4); selectors at 1024 + 16 r)."""
+    layout's own definition (chunk i = row i // 4, logical chunk (i % 4) ^ ((i // 8) % 4); selectors at 1024 + 16 r,
+    words 0-1 and 2-3 swapped in rows 8-15)."""
     from kernels.cuda_ext import _lib as lib
     from kernels.sparse import TILED_REC, compress_24, pack_24_tiled, prune_24_magnitude
 
@@ -172,5 +173,6 @@ def test_pack_24_tiled_matches_c_abi_and_round_trips():
                 r, c = rb * 16 + i // 4, (i % 4) ^ ((i // 8) % 4)
                 back_k[r, kt * 64 + c * 16:kt * 64 + c * 16 + 16] = rec[16 * i:16 * i + 16].view(np.int8)
             for r in range(16):
-                back_e[rb * 16 + r, kt * 4:kt * 4 + 4] = rec[1024 + 16 * r:1040 + 16 * r].view(np.int32)
+                stored = rec[1024 + 16 * r:1040 + 16 * r].view(np.int32)
+                back_e[rb * 16 + r, kt * 4:kt * 4 + 4] = stored[[2, 3, 0, 1]] if r >= 8 else stored
     assert np.array_equal(back_k, kept.numpy()) and np.array_equal(back_e, words.numpy())
