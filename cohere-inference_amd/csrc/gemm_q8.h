@@ -656,7 +656,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       }
     } else if constexpr (EPI == EPI_SILU_Q8) {
       // u = bf16(silu(bf16(v))), kept (as float bits) in the accumulator registers; the max |u| of each (row,
-      // MS-column block) across the lanes holding it goes to an LDS table [BM][BN/MS] (over the pipeline buffers,
+      // MS-column block) across the lanes holding it goes to an LDS table [BN/MS][BM] (over the pipeline buffers,
       // free now); then each lane reads its group's blocks and quantizes
       constexpr int CB = BN / MS;
       float* red = reinterpret_cast<float*>(smem);
@@ -681,28 +681,23 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
           }
           if constexpr (MS == 16) mx = xor32_max_pos(xor16_max_pos(mx));
           else mx = xor32_max_pos(mx);
-          if (lhi == 0) red[tok(i) * CB + (wn * TN + j * MS) / MS] = mx;
+          if (lhi == 0) red[(wn * TN + j * MS) / MS * BM + tok(i)] = mx;  // column-block major: 16 rows, 16 banks
         }
       __syncthreads();
-      // each (row, column group) maximum once, from the block table, and from it the group's scale and its reciprocal
-      // into gsc / ginv [BM][BN / qgroup]
+      // each (row, column group) maximum once, from the block table (consecutive threads take consecutive rows, so
+      // each read touches consecutive words), and from it the group's scale and its reciprocal into gsc / ginv
+      // [BM][BN / qgroup]; the maximum of non-negative values does not depend on the order
       const int blocks = p.qgroup / MS, ngroups = BN / p.qgroup;
       float* gsc = red + BM * CB;
       float* ginv = gsc + BM * (BN / 64);
       for (int id = tid; id < BM * ngroups; id += NT) {
-        const float* src = red + (id / ngroups) * CB + (id % ngroups) * blocks;
+        const int row = id % BM, g = id / BM;
+        const float* src = red + g * blocks * BM + row;
         float mx = 0.f;
-        if (blocks % 4 == 0) {
-          for (int b = 0; b < blocks; b += 4) {
-            const v4f v = *reinterpret_cast<const v4f*>(src + b);
-            mx = fmaxf(mx, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
-          }
-        } else {
-          for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, src[b]);
-        }
+        for (int b = 0; b < blocks; ++b) mx = fmaxf(mx, src[b * BM]);
         const float sc = mx > 0.f ? mx / 127.f : 1.f;
-        gsc[id] = sc;
-        ginv[id] = 1.f / sc;
+        gsc[row * ngroups + g] = sc;
+        ginv[row * ngroups + g] = 1.f / sc;
       }
       __syncthreads();
       // the int8 tile is staged in LDS past the tables and written out as whole rows (16-byte stores of 16
