@@ -145,7 +145,13 @@ DEVI void wait_stages(int after) {
 }
 
 // 16-byte chunk `c` (0..7) of row `r` of a 128-byte-row tile
-DEVI int sw128(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// The XOR key of row r: its low three bits for the 16-row reads of the 16x16 instructions; for the 32-row reads of the
+// 32x32 instructions (32 rows at chunk c, 32 at c ^ 1), rows 8-15, 16-23 and 24-31 take it XORed with 1, 2 and 3,
+// which measured free of bank conflicts on gfx950 where the plain key is not (rocprofv3 SQ_LDS_BANK_CONFLICT)
+template <int MS>
+DEVI int row_key(int r) { return MS == 32 ? (r ^ (r >> 3)) & 7 : r & 7; }
+template <int MS>
+DEVI int sw128(int r, int c) { return r * 128 + ((c ^ row_key<MS>(r)) << 4); }
 // chunk `c` (0..3) of row `r` of a 64-byte-row tile
 DEVI int sw64(int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); }
 
@@ -255,7 +261,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
     for (int j = 0; j < T::X_SLOTS / NW; ++j) {  // tokens: 8 rows of 128 B per instruction
       const int s = wave + j * NW;
       const int r = s * 8 + (lane >> 3);
-      int lc = (lane & 7) ^ (r & 7);
+      int lc = (lane & 7) ^ row_key<MS>(r);
       if (half) lc &= 3;
       dma16(p.X + (int64_t)min(m0 + r, M - 1) * p.ldx + k0 + lc * 16, base + s * 1024);
     }
@@ -265,7 +271,7 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       for (int j = 0; j < T::W_SLOTS / NW; ++j) {
         const int s = wave + j * NW;
         const int r = s * 8 + (lane >> 3);
-        int lc = (lane & 7) ^ (r & 7);
+        int lc = (lane & 7) ^ row_key<MS>(r);
         if (half) lc &= 3;
         dma16(p.W + (int64_t)(n0 + r) * K + k0 + lc * 16, wbase + s * 1024);
       }
@@ -346,9 +352,9 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
       // 16x16x64: chunk 4s + lane/16 of rows lane%16; 32x32x32: chunk 2s + lane/32 of rows lane%32
       const int lc = MS == 16 ? s * 4 + lhi : s * 2 + lhi;
 #pragma unroll
-      for (int i = 0; i < MI; ++i) F.bx[i] = *reinterpret_cast<const v4i*>(xs + sw128(wm * TM + i * MS + lrow, lc));
+      for (int i = 0; i < MI; ++i) F.bx[i] = *reinterpret_cast<const v4i*>(xs + sw128<MS>(wm * TM + i * MS + lrow, lc));
 #pragma unroll
-      for (int j = 0; j < NI; ++j) F.aw[j] = *reinterpret_cast<const v4i*>(ws + sw128(wn * TN + j * MS + lrow, lc));
+      for (int j = 0; j < NI; ++j) F.aw[j] = *reinterpret_cast<const v4i*>(ws + sw128<MS>(wn * TN + j * MS + lrow, lc));
     } else {
       const char* es = ws + T::W_STAGE;
       // B (tokens): 16x16x128 reads chunks h and 4 + h (h = lane/16); 32x32x64 step s reads 4s + h and 4s + 2 + h
@@ -360,8 +366,8 @@ __global__ void __launch_bounds__(WM* WN * 64) gemm_q8_kernel(const GemmArgs p) 
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
         const int r = wm * TM + i * MS + lrow;
-        const v4i lo = *reinterpret_cast<const v4i*>(xs + sw128(r, c0));
-        const v4i hi = *reinterpret_cast<const v4i*>(xs + sw128(r, c1));
+        const v4i lo = *reinterpret_cast<const v4i*>(xs + sw128<MS>(r, c0));
+        const v4i hi = *reinterpret_cast<const v4i*>(xs + sw128<MS>(r, c1));
         F.bx[i] = v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
 #pragma unroll
