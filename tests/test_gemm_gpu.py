@@ -95,6 +95,41 @@ def test_gemm_every_tile_same_bits(ext):
     ext.set_gemm_tile(-1)
 
 
+def test_every_tile_epilogues_match_checker(ext):
+    """Every gfx950 tile (tile shapes 64 to 256 channels wide, 16x16 and 32x32 instructions) stages its epilogue
+    through LDS with its own row swizzle: RESID, GLU and SILU_Q8 (64-column groups, so every tile holds whole
+    groups) against the checker at each tile."""
+    from kernels.cuda_ext import EPI_GLU, EPI_RESID, EPI_SILU_Q8
+
+    M, N, K = 200, 512, 640
+    _, xq, xs, wq, ws, b = _prep(M, N, K, seed=41)
+    r = torch.randn(M, N, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    args = (_np(xq), _np(xs), K, _np(wq), _np(ws), bf16_bits(b))
+    want_res = O.gemm_i8(*args, O.EPI_RESID, resid=bf16_bits(r), alpha=0.5)
+    want_glu = O.gemm_i8(*args, O.EPI_GLU)
+    want_q, want_qs = O.gemm_i8(*args, O.EPI_SILU_Q8, qgroup=64)
+    n_tiles = ext.set_gemm_tile(-1)
+    try:
+        for tile in range(n_tiles):
+            print(f"epilogues tile {tile}", flush=True)
+            ext.set_gemm_tile(tile)
+            res = r.cuda()
+            ext.gemm_i8(xq, xs, K, wq, ws, b, res, EPI_RESID, res, 0.5, None, 0)
+            glu = torch.empty(M, N // 2, dtype=torch.bfloat16, device="cuda")
+            ext.gemm_i8(xq, xs, K, wq, ws, b, glu, EPI_GLU, None, 1.0, None, 0)
+            q = torch.empty(M, N, dtype=torch.int8, device="cuda")
+            qs = torch.empty(M, N // 64, dtype=torch.float32, device="cuda")
+            ext.gemm_i8(xq, xs, K, wq, ws, b, q, EPI_SILU_Q8, None, 1.0, qs, 5)
+            torch.cuda.synchronize()
+            assert np.array_equal(bf16_bits(res), want_res), f"tile {tile}"
+            assert_bf16_close(bf16_bits(glu), want_glu)
+            dq = np.abs(_np(q).astype(np.int32) - want_q.astype(np.int32))
+            assert dq.max() <= 1 and (dq != 0).mean() < 1e-2, f"tile {tile}"
+            assert np.allclose(_np(qs), want_qs, rtol=2.0 ** -7, atol=0), f"tile {tile}"
+    finally:
+        ext.set_gemm_tile(-1)
+
+
 # ---- a3 / a4: epilogues ---------------------------------------------------------------------------------------------
 
 # 12032 rows: config 4's encoder call (32 clips of 376 frames in one call), the largest M the pipeline runs
