@@ -73,17 +73,22 @@ DEVI v8bf as_bf8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
 }
 
 // MB row blocks of 16, NS strips of 16 channels, NW waves; EP the epilogue; LN: the rows are LayerNormed first (one
-// wave per row, the same arithmetic as dec_add_ln) into LDS, and the K loop reads its activations from there
-template <int MB, int NS, int NW, bool W8, int EP, bool LN>
+// wave per row, the same arithmetic as dec_add_ln) into LDS, and the K loop reads its activations from there.
+// RB < 16 (with MB == 1): the workgroup takes RB rows only; the matrix instruction's 16 activation columns repeat
+// them (lanes 16 apart load the same addresses, so no extra bytes are fetched) and the repeats are not written.
+template <int MB, int NS, int NW, bool W8, int EP, bool LN, int RB = 16>
 __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
+  static_assert(RB == 16 || (MB == 1 && (RB == 8 || RB == 4)), "row block");
+  constexpr int ROWS = RB == 16 ? MB * 16 : RB;  // rows per workgroup
   constexpr int MAXB = (W8 ? 16 : 8) / NS;  // K blocks per wave held in registers at once (64 VGPRs of weights)
   constexpr int COLS = NS * 16, LDR = COLS + 4;
-  constexpr int RED = NW * MB * 16 * LDR * 4, XS = LN ? MB * 16 * LN_ROW : 0;
+  constexpr int RED = NW * MB * 16 * LDR * 4, XS = LN ? ROWS * LN_ROW : 0;
   // the waves' partial tiles (after the K loop) share LDS with the normalised rows (during it)
   __shared__ __attribute__((aligned(16))) char smem[RED > XS ? RED : XS];
   auto red = reinterpret_cast<float (*)[MB * 16][LDR]>(smem);
-  const int n0 = blockIdx.x * COLS, m_base = blockIdx.y * MB * 16;  // grid.y > 1: the rows split over workgroups
+  const int n0 = blockIdx.x * COLS, m_base = blockIdx.y * ROWS;  // grid.y > 1: the rows split over workgroups
   const int lane = threadIdx.x & 63, wave = wave_id(), h = lane >> 4, c16 = lane & 15;
+  const int xrow = c16 & (RB - 1);  // the activation row of this lane's matrix column
   const int nkb = p.K / KB;  // wave w takes blocks w, w + NW, ...
 
   v4f acc[NS][MB];
@@ -102,8 +107,8 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
 
   // LayerNorm prologue: each wave's rows (two loaded before the weights, so that only they are waited for ahead of
   // the weights; the rest, with MB > 1, after)
-  constexpr int RPW = LN ? MB * 16 / NW : 1, PRE = RPW < 2 ? RPW : 2;
-  static_assert(!LN || (MB * 16) % NW == 0, "rows per wave");
+  constexpr int RPW = LN ? ROWS / NW : 1, PRE = RPW < 2 ? RPW : 2;
+  static_assert(!LN || (ROWS % NW == 0 && RPW >= 1), "rows per wave");
   cohere_rows::Row<2> rows_pre[PRE];
   cohere_rows::LnParams<2> lnp;
   if constexpr (LN) {
@@ -176,9 +181,9 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
       for (int mb = 0; mb < MB; ++mb) {
         const uint16_t* xr;
         if constexpr (LN) {
-          xr = reinterpret_cast<const uint16_t*>(smem + (mb * 16 + c16) * LN_ROW) + k;
+          xr = reinterpret_cast<const uint16_t*>(smem + (mb * 16 + xrow) * LN_ROW) + k;
         } else {
-          const int m = min(m_base + mb * 16 + c16, p.M - 1);
+          const int m = min(m_base + mb * 16 + xrow, p.M - 1);
           xr = p.X + (int64_t)m * p.ldx + k;
         }
         v8bf x0, x1;
@@ -210,7 +215,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
     for (int mb = 0; mb < MB; ++mb)
       *reinterpret_cast<v4f*>(&red[wave][mb * 16 + c16][s * 16 + h * 4]) = acc[s][mb];
   __syncthreads();
-  const int rows = min(p.M - m_base, MB * 16);
+  const int rows = min(p.M - m_base, ROWS);
   for (int i = threadIdx.x; i < rows * COLS; i += NW * 64) {
     const int r = i / COLS, c = i % COLS, m = m_base + r;
     float v = red[0][r][c];
@@ -228,9 +233,26 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
 
 int g_skinny_override = -1;  // (NS << 8) | NW, tuning hook
 
+int device_cus() {
+  static const int n = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || v <= 0)
+      v = 256;
+    return v;
+  }();
+  return n;
+}
+
 template <int NS, int NW, bool W8, int EP, bool LN>
 void launch_rows(const SkinnyArgs& p, hipStream_t s) {
-  const int grid = p.N / (NS * 16), mblocks = (p.M + 15) / 16;
+  const int grid = p.N / (NS * 16), mblocks = (p.M + 15) / 16, mblocks8 = (p.M + 7) / 8;
+  if (grid * mblocks < grid * mblocks8 && grid * mblocks8 <= device_cus()) {
+    // fewer (strip, 16 rows) workgroups than CUs: one workgroup per (strip, 8 rows) instead -- twice the CUs stream
+    // the weights, and each fetches half the activations (9-32 rows of the 1024 x 1024 and 1024 x 4096 projections)
+    skinny_kernel<1, NS, NW, W8, EP, LN, 8><<<dim3(grid, mblocks8), NW * 64, 0, s>>>(p);
+    return;
+  }
   if (grid * mblocks <= 512 && mblocks > 1) {
     // few channel strips: one workgroup per (strip, 16 rows), so that every CU streams (the strip is read once per
     // 16 rows, the repeats mostly from L2 / MALL)

@@ -30,7 +30,7 @@ def _check_close(got_bits, want_bits):
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
-@pytest.mark.parametrize("M", [1, 16, 37, 64])
+@pytest.mark.parametrize("M", [1, 9, 16, 24, 32, 37, 64])
 def test_dec_w8_linear(ws, N, K, M):
     from kernels.stream_decoder import prepare_w8, w8_linear
 
@@ -45,7 +45,7 @@ def test_dec_w8_linear(ws, N, K, M):
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
-@pytest.mark.parametrize("M", [1, 24, 64])
+@pytest.mark.parametrize("M", [1, 16, 24, 32, 64])
 def test_linear_bf16(N, K, M, gpu):
     from kernels.stream_decoder import bf16_linear
 
@@ -120,7 +120,7 @@ FUSED = [(3072, 1024, True, False), (1024, 1024, False, False), (4096, 1024, Tru
 
 
 @pytest.mark.parametrize("N,K,w8,relu", FUSED)
-@pytest.mark.parametrize("M", [1, 16, 37, 64])
+@pytest.mark.parametrize("M", [1, 9, 16, 24, 32, 37, 64])
 def test_dec_linear_fused_ln_prologue(N, K, w8, relu, M, gpu):
     """LayerNorm prologue: dec_linear_fused(x, ln) has exactly the bits of dec_add_ln's LayerNorm followed by the plain
     projection (the product's own unfused path), and is within the projection bar of the oracle's LN -> linear."""
@@ -159,7 +159,7 @@ def test_dec_linear_fused_ln_prologue(N, K, w8, relu, M, gpu):
 
 
 @pytest.mark.parametrize("N,K,w8", [(1024, 1024, False), (1024, 4096, True), (1024, 4096, False)])
-@pytest.mark.parametrize("M", [1, 37, 64])
+@pytest.mark.parametrize("M", [1, 16, 24, 32, 37, 64])
 def test_dec_linear_fused_residual(N, K, w8, M, gpu):
     """Residual epilogue: y = bf16(y + bf16(x @ w^T + b)) in place, bit-identical to the projection followed by
     dec_add_ln's sum, and the sum bit-exact against the oracle's add on the kernel's projection."""
