@@ -296,8 +296,9 @@ int launch_shape(int ns, int nw, const SkinnyArgs& p, hipStream_t s) {
 
 // channels per workgroup (strips of 16) and waves per workgroup, measured on MI355X for the decoder's shapes (graph
 // replays, 1-64 rows): 8 waves; one strip while the workgroups of one strip per 16 rows stay at or below ~256, more
-// strips per workgroup beyond that (2 for 17-32 rows, 4 above, for N of 2048-8192; the head, N >= 8192, keeps 2
-// strips and whole row blocks up to 32 rows). Long K (the feed-forward's second projection) keeps one strip.
+// strips per workgroup beyond that (2 for 17-32 rows, 4 above, for N of 2048-8192; the head, N >= 8192, 2 strips
+// up to 16 rows and 4 above: at 32 rows one workgroup per (4 strips, 16 rows) normalises half the rows that one per
+// (2 strips, 32 rows) did, config 4 end to end +0.3 %). Long K (the feed-forward's second projection) keeps one strip.
 void choose_shape(int N, int K, int M, int& ns, int& nw) {
   if (g_skinny_override > 0) {
     ns = g_skinny_override >> 8;
@@ -306,7 +307,7 @@ void choose_shape(int N, int K, int M, int& ns, int& nw) {
   }
   nw = 8;
   if (K >= 2048 || N < 2048) ns = 1;
-  else if (N >= 8192) ns = M > 32 ? 4 : 2;
+  else if (N >= 8192) ns = M > 16 ? 4 : 2;
   else ns = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
   while (ns > 1 && N % (ns * 16) != 0) ns >>= 1;
 }
