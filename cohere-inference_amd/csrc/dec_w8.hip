@@ -76,11 +76,18 @@ DEVI v8bf as_bf8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
 // wave per row, the same arithmetic as dec_add_ln) into LDS, and the K loop reads its activations from there.
 // RB < 16 (with MB == 1): the workgroup takes RB rows only; the matrix instruction's 16 activation columns repeat
 // them (lanes 16 apart load the same addresses, so no extra bytes are fetched) and the repeats are not written.
-template <int MB, int NS, int NW, bool W8, int EP, bool LN, int RB = 16>
+// BPW > 0: K holds exactly NW * BPW blocks, so every wave's loads are unconditional: without a LayerNorm the
+// activations (L2 hits, written by the previous launch) are issued first, then the weights (from HBM), so that waiting
+// for a block's activations never waits for weights (loads complete in order), and each matrix instruction waits for
+// its own block's weights only. (Conditional loads made the compiler wait for all weights at the branches' join and
+// then fetch each block's activations as a round trip of its own.)
+template <int MB, int NS, int NW, bool W8, int EP, bool LN, int RB = 16, int BPW = 0>
 __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   static_assert(RB == 16 || (MB == 1 && (RB == 8 || RB == 4)), "row block");
   constexpr int ROWS = RB == 16 ? MB * 16 : RB;  // rows per workgroup
-  constexpr int MAXB = (W8 ? 16 : 8) / NS;  // K blocks per wave held in registers at once (64 VGPRs of weights)
+  constexpr int MAXB = BPW > 0 ? BPW : (W8 ? 16 : 8) / NS;  // K blocks per wave in registers at once (<= 64 VGPRs)
+  static_assert(BPW == 0 || BPW * NS * (W8 ? 1 : 2) <= 16, "weight registers");
+  constexpr bool XPRE = BPW > 0 && !LN;  // the activations loaded ahead of the weights
   constexpr int COLS = NS * 16, LDR = COLS + 4;
   constexpr int RED = NW * MB * 16 * LDR * 4, XS = LN ? ROWS * LN_ROW : 0;
   // the waves' partial tiles (after the K loop) share LDS with the normalised rows (during it)
@@ -123,10 +130,24 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   bool first = true;
   for (int b0 = wave; b0 < nkb; b0 += NW * MAXB) {
     uint4 wreg[MAXB][NS][W8 ? 1 : 2];
+    uint4 xreg[XPRE ? MAXB : 1][XPRE ? MB : 1][2];
+    if constexpr (XPRE) {
+#pragma unroll
+      for (int b = 0; b < MAXB; ++b) {
+        const int64_t k = (int64_t)(b0 + NW * b) * KB;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const uint16_t* xr = p.X + (int64_t)min(m_base + mb * 16 + xrow, p.M - 1) * p.ldx + k;
+          xreg[b][mb][0] = *reinterpret_cast<const uint4*>(xr + (W8 ? 16 * h : 8 * h));
+          xreg[b][mb][1] = *reinterpret_cast<const uint4*>(xr + (W8 ? 16 * h + 8 : 32 + 8 * h));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // the activations' loads stay ahead of the weights'
+    }
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
       const int kb = b0 + NW * b;
-      if (kb < nkb) {
+      if (BPW > 0 || kb < nkb) {
         const int64_t k = (int64_t)kb * KB;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -141,6 +162,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
         }
       }
     }
+    if constexpr (BPW > 0) __builtin_amdgcn_sched_barrier(0);  // every load issued before the first product
     if constexpr (LN) {
       if (first) {
         // every wave reaches this (the caller guarantees at least NW blocks of K)
@@ -163,7 +185,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
 #pragma unroll
     for (int b = 0; b < MAXB; ++b) {
       const int kb = b0 + NW * b;
-      if (kb >= nkb) break;
+      if (BPW == 0 && kb >= nkb) break;
       const int64_t k = (int64_t)kb * KB;
       v8bf w0[NS], w1[NS];
 #pragma unroll
@@ -188,13 +210,16 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
         }
         v8bf x0, x1;
         if constexpr (W8) {
-          const uint4 lo = *reinterpret_cast<const uint4*>(xr + 16 * h);      // logical 0..7 of this 16-block
-          const uint4 hi = *reinterpret_cast<const uint4*>(xr + 16 * h + 8);  // logical 8..15
+          const uint4 lo = XPRE ? xreg[XPRE ? b : 0][XPRE ? mb : 0][0]
+                                : *reinterpret_cast<const uint4*>(xr + 16 * h);  // logical 0..7 of this 16-block
+          const uint4 hi = XPRE ? xreg[XPRE ? b : 0][XPRE ? mb : 0][1]
+                                : *reinterpret_cast<const uint4*>(xr + 16 * h + 8);  // logical 8..15
           x0 = as_bf8(lo.x, hi.x, lo.y, hi.y);  // pairs (0,1) (8,9) (2,3) (10,11)
           x1 = as_bf8(lo.z, hi.z, lo.w, hi.w);  // pairs (4,5) (12,13) (6,7) (14,15)
         } else {
-          const uint4 a = *reinterpret_cast<const uint4*>(xr + 8 * h);
-          const uint4 c = *reinterpret_cast<const uint4*>(xr + 32 + 8 * h);
+          const uint4 a = XPRE ? xreg[XPRE ? b : 0][XPRE ? mb : 0][0] : *reinterpret_cast<const uint4*>(xr + 8 * h);
+          const uint4 c = XPRE ? xreg[XPRE ? b : 0][XPRE ? mb : 0][1]
+                               : *reinterpret_cast<const uint4*>(xr + 32 + 8 * h);
           x0 = as_bf8(a.x, a.y, a.z, a.w);
           x1 = as_bf8(c.x, c.y, c.z, c.w);
         }
@@ -244,26 +269,45 @@ int device_cus() {
   return n;
 }
 
+// the kernel with every wave's loads unconditional when K splits into exactly 2 or 8 blocks per wave (the decoder's
+// 1024 and 4096) and the registers fit; otherwise the general loop
+template <int MB, int NS, int NW, bool W8, int EP, bool LN, int RB = 16>
+void launch_k(dim3 grid, const SkinnyArgs& p, hipStream_t s) {
+  constexpr int WR = NS * (W8 ? 1 : 2);  // weight registers (x4) per block
+  const int nkb = p.K / KB;
+  if (nkb == 2 * NW && (LN || MB <= 4)) {
+    skinny_kernel<MB, NS, NW, W8, EP, LN, RB, 2><<<grid, NW * 64, 0, s>>>(p);
+    return;
+  }
+  if constexpr (8 * WR <= 16 && MB == 1) {
+    if (nkb == 8 * NW) {
+      skinny_kernel<MB, NS, NW, W8, EP, LN, RB, 8><<<grid, NW * 64, 0, s>>>(p);
+      return;
+    }
+  }
+  skinny_kernel<MB, NS, NW, W8, EP, LN, RB><<<grid, NW * 64, 0, s>>>(p);
+}
+
 template <int NS, int NW, bool W8, int EP, bool LN>
 void launch_rows(const SkinnyArgs& p, hipStream_t s) {
   const int grid = p.N / (NS * 16), mblocks = (p.M + 15) / 16, mblocks8 = (p.M + 7) / 8;
   if (grid * mblocks < grid * mblocks8 && grid * mblocks8 <= device_cus()) {
     // fewer (strip, 16 rows) workgroups than CUs: one workgroup per (strip, 8 rows) instead -- twice the CUs stream
     // the weights, and each fetches half the activations (9-32 rows of the 1024 x 1024 and 1024 x 4096 projections)
-    skinny_kernel<1, NS, NW, W8, EP, LN, 8><<<dim3(grid, mblocks8), NW * 64, 0, s>>>(p);
+    launch_k<1, NS, NW, W8, EP, LN, 8>(dim3(grid, mblocks8), p, s);
     return;
   }
   if (grid * mblocks <= 512 && mblocks > 1) {
     // few channel strips: one workgroup per (strip, 16 rows), so that every CU streams (the strip is read once per
     // 16 rows, the repeats mostly from L2 / MALL)
-    skinny_kernel<1, NS, NW, W8, EP, LN><<<dim3(grid, mblocks), NW * 64, 0, s>>>(p);
+    launch_k<1, NS, NW, W8, EP, LN>(dim3(grid, mblocks), p, s);
     return;
   }
   switch (mblocks) {
-    case 1: skinny_kernel<1, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
-    case 2: skinny_kernel<2, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
-    case 3: skinny_kernel<3, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
-    default: skinny_kernel<4, NS, NW, W8, EP, LN><<<grid, NW * 64, 0, s>>>(p); break;
+    case 1: launch_k<1, NS, NW, W8, EP, LN>(dim3(grid), p, s); break;
+    case 2: launch_k<2, NS, NW, W8, EP, LN>(dim3(grid), p, s); break;
+    case 3: launch_k<3, NS, NW, W8, EP, LN>(dim3(grid), p, s); break;
+    default: launch_k<4, NS, NW, W8, EP, LN>(dim3(grid), p, s); break;
   }
 }
 
