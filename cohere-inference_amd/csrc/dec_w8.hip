@@ -88,6 +88,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   constexpr int MAXB = BPW > 0 ? BPW : (W8 ? 16 : 8) / NS;  // K blocks per wave in registers at once (<= 64 VGPRs)
   static_assert(BPW == 0 || BPW * NS * (W8 ? 1 : 2) <= 16, "weight registers");
   constexpr bool XPRE = BPW > 0 && !LN;  // the activations loaded ahead of the weights
+  constexpr bool FULLROW = LN && BPW * NW * KB == LN_K;  // K is the LayerNorm's full 1024: unguarded row loads
   constexpr int COLS = NS * 16, LDR = COLS + 4;
   constexpr int RED = NW * MB * 16 * LDR * 4, XS = LN ? ROWS * LN_ROW : 0;
   // the waves' partial tiles (after the K loop) share LDS with the normalised rows (during it)
@@ -119,11 +120,11 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
   cohere_rows::Row<2> rows_pre[PRE];
   cohere_rows::LnParams<2> lnp;
   if constexpr (LN) {
-    lnp = cohere_rows::load_ln<2>(p.lnw, p.lnb, p.K, lane);
+    lnp = cohere_rows::load_ln<2, FULLROW>(p.lnw, p.lnb, p.K, lane);
 #pragma unroll
     for (int j = 0; j < PRE; ++j) {
       const int m = min(m_base + wave * RPW + j, p.M - 1);
-      cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j]);
+      cohere_rows::load_row<2, FULLROW>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j]);
     }
   }
 
@@ -173,7 +174,7 @@ __global__ void __launch_bounds__(NW * 64) skinny_kernel(const SkinnyArgs p) {
           cohere_rows::Row<2> r = rows_pre[j % PRE];
           if (j + PRE < RPW) {
             const int m = min(m_base + wave * RPW + j + PRE, p.M - 1);
-            cohere_rows::load_row<2>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j % PRE]);
+            cohere_rows::load_row<2, FULLROW>(p.X + (int64_t)m * p.ldx, p.K, lane, rows_pre[j % PRE]);
           }
           cohere_rows::ln_row<2>(r, p.K, lane, lnp, p.eps);
           cohere_rows::store_row<2>(r, p.K, lane, reinterpret_cast<uint16_t*>(smem + (wave * RPW + j) * LN_ROW));

@@ -10,13 +10,15 @@ struct Row {
   float v[VEC][8];
 };
 
-template <int VEC>
+// FULL: cols == VEC * 512, so every lane's chunks are in the row and the loads need no guard (a guarded load is a
+// branch, and the compiler waits for every load in flight where the branches join)
+template <int VEC, bool FULL = false>
 DEVI void load_row(const uint16_t* x, int cols, int lane, Row<VEC>& r) {
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
     const int c = (i * 64 + lane) * 8;
     uint4 u = make_uint4(0, 0, 0, 0);
-    if (c < cols) u = *reinterpret_cast<const uint4*>(x + c);
+    if (FULL || c < cols) u = *reinterpret_cast<const uint4*>(x + c);
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -55,14 +57,14 @@ struct LnParams {
   uint4 w[VEC], b[VEC];
 };
 
-template <int VEC>
+template <int VEC, bool FULL = false>
 DEVI LnParams<VEC> load_ln(const uint16_t* w, const uint16_t* b, int cols, int lane) {
   LnParams<VEC> p;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) {
     const int c = (i * 64 + lane) * 8;
-    p.w[i] = c < cols ? *reinterpret_cast<const uint4*>(w + c) : make_uint4(0, 0, 0, 0);
-    p.b[i] = c < cols ? *reinterpret_cast<const uint4*>(b + c) : make_uint4(0, 0, 0, 0);
+    p.w[i] = FULL || c < cols ? *reinterpret_cast<const uint4*>(w + c) : make_uint4(0, 0, 0, 0);
+    p.b[i] = FULL || c < cols ? *reinterpret_cast<const uint4*>(b + c) : make_uint4(0, 0, 0, 0);
   }
   return p;
 }
