@@ -28,14 +28,15 @@ constexpr int HD = 128;  // head size
 // ---- embedding and residual LayerNorms: one wave per row ------------------------------------------------------------
 
 // one row's embedding by one wave: x = LN0(bf16(emb[t] + ptab[p])), h = LN1(x)
-template <int VEC>
+// FULL: width == VEC * 512 (the loads then need no per-lane guard)
+template <int VEC, bool FULL = false>
 DEVI void embed_row(int64_t t, int p, const uint16_t* emb, const uint16_t* ptab, const uint16_t* w0,
                     const uint16_t* b0, float eps0, const uint16_t* w1, const uint16_t* b1, float eps1, uint16_t* xr,
                     uint16_t* hr, int width, int lane) {
-  const LnParams<VEC> p0 = load_ln<VEC>(w0, b0, width, lane), p1 = load_ln<VEC>(w1, b1, width, lane);
+  const LnParams<VEC> p0 = load_ln<VEC, FULL>(w0, b0, width, lane), p1 = load_ln<VEC, FULL>(w1, b1, width, lane);
   Row<VEC> e, q;
-  load_row<VEC>(emb + t * width, width, lane, e);
-  load_row<VEC>(ptab + (int64_t)p * width, width, lane, q);
+  load_row<VEC, FULL>(emb + t * width, width, lane, e);
+  load_row<VEC, FULL>(ptab + (int64_t)p * width, width, lane, q);
 #pragma unroll
   for (int i = 0; i < VEC; ++i)
 #pragma unroll
@@ -471,7 +472,7 @@ struct PickEmbed {
   uint8_t* flags;  // host-mapped end flags (null: none)
 };
 
-template <int EVEC>
+template <int EVEC, bool EFULL = false>
 __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restrict__ logits, int V,
                                                        const int32_t* __restrict__ active, int dummy, int64_t* tok,
                                                        int32_t* pos, uint8_t* finished, const int64_t* forced, int FP,
@@ -587,7 +588,7 @@ __global__ void __launch_bounds__(256) dec_pick_kernel(const uint16_t* __restric
   if constexpr (EVEC > 0) {
     __syncthreads();
     if (tid < 64)
-      embed_row<EVEC>(s_tok, s_pos, pe.emb, pe.ptab, pe.w0, pe.b0, pe.eps0, pe.w1, pe.b1, pe.eps1,
+      embed_row<EVEC, EFULL>(s_tok, s_pos, pe.emb, pe.ptab, pe.w0, pe.b0, pe.eps0, pe.w1, pe.b1, pe.eps1,
                       pe.x + (int64_t)r * pe.width, pe.h + (int64_t)r * pe.width, pe.width, tid);
   }
   (void)pad;
@@ -791,14 +792,15 @@ extern "C" int cohere_dec_pick_embed(const uint16_t* logits, int64_t rows, int64
   if (rows == 0) return 0;
   const PickEmbed pe{emb, ptab, w0, b0, w1, b1, eps0, eps1, x, h, (int)width, flags_dev};
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-#define PICK(VV)                                                                                                   \
-  dec_pick_kernel<VV><<<(unsigned)rows, 256, 0, st>>>(logits, (int)V, active, (int)dummy, tok, pos, finished, forced, \
-                                                      (int)FP, plen, limit, out, (int)OUT, pad, eos, pe)
+#define PICK(VV, F)                                                                                                \
+  dec_pick_kernel<VV, F><<<(unsigned)rows, 256, 0, st>>>(logits, (int)V, active, (int)dummy, tok, pos, finished,      \
+                                                         forced, (int)FP, plen, limit, out, (int)OUT, pad, eos, pe)
+  const bool full = width % 512 == 0;  // vec_of(width) chunks of 512, all whole
   switch (vec_of(width)) {
-    case 1: PICK(1); break;
-    case 2: PICK(2); break;
-    case 3: PICK(3); break;
-    default: PICK(4); break;
+    case 1: if (full) PICK(1, true); else PICK(1, false); break;
+    case 2: if (full) PICK(2, true); else PICK(2, false); break;
+    case 3: if (full) PICK(3, true); else PICK(3, false); break;
+    default: if (full) PICK(4, true); else PICK(4, false); break;
   }
 #undef PICK
   return cohere::check_launch("dec_pick_embed");
