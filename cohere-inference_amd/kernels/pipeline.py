@@ -84,6 +84,7 @@ class _Decoding:
         self.first_step: dict[int, int] = {}
         self.inflight: deque = deque()
         self.steps = 0
+        self.limit: dict[int, int] = {}  # a slot's step (counted from its admission) that ends it by the token limit
         self.bucket, self.stale = 1, True
         self.rows_host = torch.zeros(dec.slots + 1, dec.out.shape[1], dtype=torch.long).pin_memory()
 
@@ -93,18 +94,29 @@ class _Decoding:
         for s, p in zip(slots, pieces):
             self.holder[s] = p
             self.first_step[s] = self.steps
+            # the pick ends a row at its step `plen - 1 + max_new` after admission, if no end token came first
+            self.limit[s] = len(p.prompt) - 1 + (p.max_new or dec.max_new_tokens)
         self.active += slots
         self.stale = True
 
-    def step(self) -> None:
+    def chunk(self) -> int:
+        """Steps to launch at once: the decoder's chunk, but never past the step at which an active row reaches its
+        token limit, so that rows ending by the limit are seen as early as with single steps (a row ending by its end
+        token is seen up to a chunk later, and it is stepped meanwhile as between any launch and its harvest)."""
+        if not self.active:
+            return 1
+        left = min(self.limit[s] - (self.steps - self.first_step[s]) for s in self.active)
+        return max(1, min(self.dec.chunk, left))
+
+    def step(self, n: int = 1) -> None:
         if self.stale:
             self.bucket = self.dec.set_active(self.active)
             self.stale = False
-        self.dec.step(self.bucket)
+        self.dec.step(self.bucket, n)
         ev = torch.cuda.Event()
         ev.record(self.dec.stream)
-        self.inflight.append((self.steps, ev))
-        self.steps += 1
+        self.inflight.append((self.steps + n - 1, ev))  # the flags after the last of the n steps
+        self.steps += n
 
     def harvest(self) -> list[tuple[int, _Piece]]:
         """(slot, piece) of every piece found ended, its tokens set; the slots are free again."""
@@ -227,8 +239,9 @@ class Pipeline:
                     dec.stream.wait_stream(torch.cuda.current_stream())
                     run.admit(slots, chunk, lengths)
                     queue, room = queue[len(chunk):], room - len(chunk)
-            run.step()
-            self.stats["steps"] += 1
+            n = 1 if queue and free else run.chunk()  # single steps while pieces wait for a slot
+            run.step(n)
+            self.stats["steps"] += n
             for s, p in run.harvest():
                 result[p.k] = p.tokens
                 free.append(s)
@@ -357,8 +370,11 @@ class Pipeline:
                     self._release(slots, chunk, exc)
             try:
                 if run.active:
-                    run.step()
-                    self.stats["steps"] += 1
+                    with self._cv:
+                        waiting = bool(self._waiting or self._encoded)
+                    n = 1 if waiting else run.chunk()  # single steps while pieces are on their way in
+                    run.step(n)
+                    self.stats["steps"] += n
                 ended = run.harvest()
                 if not run.active:
                     run.drain()

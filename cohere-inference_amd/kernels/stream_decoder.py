@@ -155,7 +155,7 @@ class StreamDecoder:
 
     def __init__(self, model, slots: int = 128, max_new_tokens: int = 448, max_prompt: int = 16,
                  max_audio_s: float = 36.0, buckets=None, int8: bool = False, frames: int | None = None,
-                 capture: bool = True, fused: bool | None = None):
+                 capture: bool = True, fused: bool | None = None, chunk: int = 4):
         dec, cfg = model.model.decoder, model.config
         self.model, self.int8 = model, int8
         self.buckets = tuple(sorted(b for b in (buckets or self.BUCKETS) if b <= slots))
@@ -236,6 +236,10 @@ class StreamDecoder:
         self._embed_stale, self._embed_rows = True, 0
         self.programs = {b: self._program(b) for b in self.buckets}
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        # `chunk` consecutive steps recorded into one graph per bucket as well (step(bucket, chunk)): a graph boundary
+        # costs a few microseconds of idle GPU, which one replay per step pays every step
+        self.chunk = max(1, int(chunk))
+        self.chunk_graphs: dict[int, torch.cuda.CUDAGraph] = {}
         if capture:
             self._capture()
 
@@ -335,6 +339,13 @@ class StreamDecoder:
                     for op in self.programs[b]:  # the program only: step() adds the embedding when the rows change
                         op()
                 self.graphs[b] = g
+                if self.chunk > 1:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=self.stream):
+                        for _ in range(self.chunk):
+                            for op in self.programs[b]:
+                                op()
+                    self.chunk_graphs[b] = g
         self.reset()
         self.stream.synchronize()
 
@@ -429,17 +440,22 @@ class StreamDecoder:
         self._embed_stale = True
         return b
 
-    def step(self, bucket: int) -> None:
-        """One decoding step of the first `bucket` active rows (a graph replay on the decoder stream). With the fused
-        program the rows' embeddings come from the previous step's pick; after admit / set_active / reset, or on a
-        different bucket, they are computed first."""
+    def step(self, bucket: int, n: int = 1) -> None:
+        """`n` decoding steps of the first `bucket` active rows (graph replays on the decoder stream; n == chunk is
+        one replay of the chunk graph). With the fused program the rows' embeddings come from the previous step's
+        pick; after admit / set_active / reset, or on a different bucket, they are computed first."""
         with torch.cuda.stream(self.stream):
             if bucket in self.graphs:
                 if self.fused and (self._embed_stale or bucket != self._embed_rows):
                     self._embed(bucket)
-                self.graphs[bucket].replay()
+                if n > 1 and n == self.chunk and bucket in self.chunk_graphs:
+                    self.chunk_graphs[bucket].replay()
+                else:
+                    for _ in range(n):
+                        self.graphs[bucket].replay()
             else:
-                self._run(bucket)
+                for _ in range(n):
+                    self._run(bucket)
             self._embed_stale, self._embed_rows = False, bucket
 
     def weight_bytes(self) -> int:
