@@ -1,8 +1,9 @@
 """End-to-end transcription on gfx950: audio pieces -> log-mel features -> packed encoder -> cross-attention caches ->
 greedy decoding with continuous batching -> token ids (the call surface of the reference's kernels/pipeline.py).
 
-Two ways in, one decoding engine (_Decoding: the active slots, the pieces they hold, the steps in flight and the
-end flags read LAG steps behind, so the GPU never waits for the host):
+Two ways in, one decoding engine (_Decoding: the active slots, the pieces they hold, the steps in flight -- launched
+in chunks of the decoder's `chunk` steps while no piece waits, one graph replay each -- and the end flags read LAG
+launches behind, so the GPU never waits for the host):
 
   submit(pieces, prompt, max_new) -> Future   a service: an encoder thread takes waiting pieces in chunks of at most
                                               CHUNK_FRAMES encoder frames (as many as there are free decoder slots),
